@@ -1,0 +1,132 @@
+/*
+ * exl3_hip.h -- C-ABI of the MI355X (gfx950) EXL3 packed-weight linear layer.
+ *
+ * Plain pointers and sizes; every pointer named "device" is HIP device memory
+ * owned by the caller.  Work is enqueued on the given stream (0 = the null
+ * stream) and the functions return without synchronising unless stated.
+ * No function throws; every one returns an exl3_status.
+ *
+ * Reference interfaces replaced (paths are in the reference checkout):
+ *   exl3_hip_mul_mat      <- ggml_exl3_mul_mat        src/exl3-ggml.cpp:51-92,
+ *                            declared include/exl3-block.h:46, dispatched from
+ *                            ggml_compute_forward_mul_mat (patches/llama-exl3.patch:44-51);
+ *                            device twin op_exl3_matmul src/exl3-htp.c:159-232;
+ *                            scalar model exl3_iface_matmul src/hexagon/exl3_iface.idl:13-15
+ *   exl3_hip_decode       <- exl3::decode_inner(_slice) src/exl3_codec.cpp:123-145
+ *                            (and exl3_iface_decode src/hexagon/exl3_iface.idl:5-7)
+ *   exl3_hip_reconstruct  <- exl3::reconstruct(_slice)  src/exl3_codec.cpp:169-204
+ *   exl3_hip_codebook     <- exl3::decode_codebook      src/exl3_codec.cpp:68-86
+ *   exl3_hip_hadamard128  <- exl3::hadamard128          src/exl3_codec.cpp:147-167
+ *   exl3_hip_pack_records <- record assembly tests/test-exl3-graph.cpp:110-118,
+ *                            tools/export_native_gguf.py:27-36
+ *   exl3_hip_validate_records <- ggml_validate_row_data EXL3 case
+ *                            patches/llama-exl3.patch:327-338
+ *   exl3_hip_supports_mul_mat <- supports_op predicates patches/llama-exl3.patch:81-84,225-235
+ */
+#ifndef EXL3_HIP_H
+#define EXL3_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EXL3_HIP_VERSION 10000u /* major * 10000 + minor * 100 + patch */
+
+typedef enum exl3_status {
+    EXL3_OK = 0,
+    EXL3_INVAL_PARAMS = 1,       /* shape / rate / codebook / stride rejected (HTP_STATUS_INVAL_PARAMS) */
+    EXL3_NO_SUPPORT = 2,         /* valid request this build does not implement (HTP_STATUS_NO_SUPPORT) */
+    EXL3_WORKSPACE_TOO_SMALL = 3,/* caller workspace below exl3_hip_mul_mat_workspace_bytes() */
+    EXL3_HIP_ERROR = 4           /* a HIP runtime call failed (HTP_STATUS_INTERNAL_ERR) */
+} exl3_status;
+
+typedef enum exl3_dtype { EXL3_F32 = 0, EXL3_F16 = 1 } exl3_dtype;
+
+/* codebook ids match exl3::Codebook (include/exl3_codec.h) */
+typedef enum exl3_codebook { EXL3_CB_3INST = 0, EXL3_CB_MCG = 1, EXL3_CB_MUL1 = 2 } exl3_codebook;
+
+typedef enum exl3_layout {
+    EXL3_LAYOUT_UPSTREAM_TILES = 0, /* [k/16][n/16][16*bits] u16, the .trellis tensor */
+    EXL3_LAYOUT_RECORDS = 1         /* 128x128 group records, include/exl3-block.h */
+} exl3_layout;
+
+unsigned exl3_hip_version(void);
+const char *exl3_hip_status_string(exl3_status status);
+
+/* Largest row count served by the register-decode GEMV kernel; larger row
+ * counts use the LDS-decode MFMA GEMM kernel. */
+size_t exl3_hip_gemv_max_rows(void);
+
+/* 1 when exl3_hip_mul_mat accepts this problem: bits 1..8, codebook 0..2,
+ * k and n nonzero multiples of 128, 1 <= rows <= 65536, dtypes F32/F16. */
+int exl3_hip_supports_mul_mat(unsigned bits, unsigned codebook, size_t k, size_t n, size_t rows,
+                              exl3_dtype xt, exl3_dtype yt);
+
+/* Device workspace bytes exl3_hip_mul_mat needs for this problem.  The
+ * workspace holds per-call staging and self-resetting completion counters:
+ * it must be zero-filled once before its first use (exl3_hip_workspace_init)
+ * and must not be shared by calls that may run concurrently. */
+size_t exl3_hip_mul_mat_workspace_bytes(size_t k, size_t n, size_t rows);
+exl3_status exl3_hip_workspace_init(void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/*
+ * y[r][j] = sv[j] * H128( sum_i H128(x[r] * su)[i] * W_hat[i][j] )   (0 <= r < rows)
+ * i.e. y = x . diag(su) H W_hat H diag(sv), the EXL3 linear layer, with su taken
+ * from record (0, kb) and sv from record (nb, 0) as src/exl3-ggml.cpp:60-90 does.
+ *   records      device, (n/128)*(k/128) records of exl3_group_bytes(bits), 16-byte aligned
+ *   bits         1..8; codebook 0..2 (the reference's ggml op uses mul1 = 2)
+ *   x            device, rows x k of xt, row stride x_row_stride elements (>= k)
+ *   y            device, rows x n of yt, row stride y_row_stride elements (>= n)
+ *   workspace    device, >= exl3_hip_mul_mat_workspace_bytes(k, n, rows), zero-filled
+ *                before first use; NULL -> an internal per-(device, stream)
+ *                workspace is allocated on first use and kept
+ * Deterministic: the same inputs give the same bits on every call.
+ */
+exl3_status exl3_hip_mul_mat(const void *records, unsigned bits, unsigned codebook, size_t k, size_t n,
+                             const void *x, exl3_dtype xt, size_t rows, size_t x_row_stride,
+                             void *y, exl3_dtype yt, size_t y_row_stride,
+                             void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Decode packed weights to row-major fp16 bits out[k][column_count] for
+ * columns [first_column, first_column + column_count), bit-exact with
+ * exl3::decode_inner_slice.  UPSTREAM_TILES: k, n, first and count multiples
+ * of 16; RECORDS: multiples of 128.  out is device memory. */
+exl3_status exl3_hip_decode(const void *src, exl3_layout layout, unsigned bits, unsigned codebook,
+                            size_t k, size_t n, size_t first_column, size_t column_count,
+                            uint16_t *out, hipStream_t stream);
+
+/* Original-basis weights diag(su) H W_hat H diag(sv) as fp16 bits out[k][column_count],
+ * bit-exact with exl3::reconstruct_slice.  UPSTREAM_TILES takes su (k) and sv (n)
+ * fp16 device vectors; RECORDS reads them from the records (su/sv may be NULL).
+ * k, n, first_column, column_count multiples of 128. */
+exl3_status exl3_hip_reconstruct(const void *src, exl3_layout layout, const uint16_t *su,
+                                 const uint16_t *sv, unsigned bits, unsigned codebook, size_t k,
+                                 size_t n, size_t first_column, size_t column_count, uint16_t *out,
+                                 hipStream_t stream);
+
+/* out[i] = fp16 codebook value of states[i], bit-exact with exl3::decode_codebook. */
+exl3_status exl3_hip_codebook(const uint16_t *states, size_t count, unsigned codebook, uint16_t *out,
+                              hipStream_t stream);
+
+/* In-place orthonormal H128 over each consecutive 128 fp32 values (count % 128 == 0),
+ * bit-exact with exl3::hadamard128. */
+exl3_status exl3_hip_hadamard128(float *values, size_t count, hipStream_t stream);
+
+/* Upstream tiles [k/16][n/16][16*bits] + su[k] + sv[n] -> records. */
+exl3_status exl3_hip_pack_records(const uint16_t *packed, const uint16_t *su, const uint16_t *sv,
+                                  unsigned bits, size_t k, size_t n, void *records, hipStream_t stream);
+
+/* *result (device int) = 1 when every su/sv value of every record is finite,
+ * 0 otherwise; EXL3_INVAL_PARAMS when nbytes is not a whole number of records. */
+exl3_status exl3_hip_validate_records(const void *records, size_t nbytes, unsigned bits, int *result,
+                                      hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EXL3_HIP_H */

@@ -1,0 +1,69 @@
+"""CPU checks of the drop-in boundary: the product library loads and exports
+every function include/*.h declares; the oracle agrees with the compiled
+reference codec (when the reference build exists)."""
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+LIB = ROOT / "xiaomi-hexagon-exl3_amd" / "libexl3_hip.so"
+
+
+def declared_c_functions():
+    text = (ROOT / "include" / "exl3_hip.h").read_text()
+    return sorted(set(re.findall(r"\b(exl3_hip_\w+)\s*\(", text)))
+
+
+def exported_symbols():
+    out = subprocess.run(["nm", "-D", "--defined-only", str(LIB)], capture_output=True, text=True, check=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if line.strip()}
+
+
+def test_library_loads_and_exports_c_abi():
+    import conftest
+    amd = conftest.load_amd()   # loads libexl3_hip.so, binds every prototype; no GPU call
+    syms = exported_symbols()
+    declared = declared_c_functions()
+    assert len(declared) >= 13
+    missing = [f for f in declared if f not in syms]
+    assert not missing, missing
+    assert set(amd.EXPORTS) == set(declared)
+    assert amd.lib().exl3_hip_version() == 10000
+    assert amd.lib().exl3_hip_gemv_max_rows() == 8
+
+
+def test_library_exports_codec_api():
+    out = subprocess.run(["nm", "-DC", "--defined-only", str(LIB)], capture_output=True, text=True, check=True).stdout
+    text = (ROOT / "include" / "exl3_codec.h").read_text()
+    names = sorted(set(re.findall(r"^\w[\w\s\*]*?\b(\w+)\(", text, re.M)))
+    assert {"decode_inner", "reconstruct_slice", "hadamard128", "decode_codebook"} <= set(names)
+    for name in names:
+        assert f"exl3::{name}(" in out, name
+
+
+def test_host_side_status_and_planning():
+    import conftest
+    L = conftest.load_amd().lib()
+    # pure host logic, no device work
+    assert L.exl3_hip_supports_mul_mat(4, 2, 14336, 4096, 1, 1, 1) == 1
+    assert L.exl3_hip_supports_mul_mat(0, 2, 14336, 4096, 1, 1, 1) == 0
+    assert L.exl3_hip_supports_mul_mat(4, 3, 14336, 4096, 1, 1, 1) == 0
+    assert L.exl3_hip_supports_mul_mat(4, 2, 14300, 4096, 1, 1, 1) == 0
+    assert L.exl3_hip_supports_mul_mat(4, 2, 128, 128, 0, 1, 1) == 0
+    assert L.exl3_hip_mul_mat_workspace_bytes(14336, 4096, 1) > 0
+    assert L.exl3_hip_mul_mat_workspace_bytes(14336, 4096, 512) > L.exl3_hip_mul_mat_workspace_bytes(14336, 4096, 8)
+    assert L.exl3_hip_mul_mat_workspace_bytes(100, 4096, 1) == 0
+    # rejected arguments never reach the device
+    assert L.exl3_hip_mul_mat(None, 4, 2, 128, 128, None, 1, 1, 128, None, 0, 128, None, 0, None) == 1
+    assert L.exl3_hip_decode(None, 0, 4, 2, 16, 16, 0, 16, None, None) == 1
+    assert L.exl3_hip_hadamard128(None, 100, None) == 1
+    assert L.exl3_hip_status_string(3) == b"workspace too small"
+
+
+@pytest.mark.skipif(not (ROOT / "oracle" / "_ref" / "check_ref").exists(), reason="reference build absent")
+def test_oracle_exhaustive_vs_compiled_reference():
+    r = subprocess.run([str(ROOT / "oracle" / "_ref" / "check_ref")], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "0 mismatches over 2^32" in r.stdout

@@ -1,0 +1,181 @@
+// exl3_api.cpp -- the C-ABI of include/exl3_hip.h: argument checks, workspace
+// management and dispatch to the gfx950 kernels.  Checks mirror the reference's
+// preconditions (src/exl3-ggml.cpp:56-57, src/exl3_codec.cpp:12-19,117-135,
+// patches/llama-exl3.patch:81-84,225-235) and turn them into status codes.
+#include "exl3_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <map>
+#include <mutex>
+#include <utility>
+
+#include "exl3_launch.hpp"
+
+namespace {
+
+exl3_status from_hip(hipError_t e) { return e == hipSuccess ? EXL3_OK : EXL3_HIP_ERROR; }
+
+bool valid_rate(unsigned bits, unsigned cb) { return bits >= 1 && bits <= 8 && cb <= 2; }
+bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
+bool valid_dtype(exl3_dtype t) { return t == EXL3_F32 || t == EXL3_F16; }
+size_t dtype_size(exl3_dtype t) { return t == EXL3_F16 ? 2 : 4; }
+
+constexpr size_t kMaxRows = 65536;
+constexpr size_t kMaxDim = (size_t)1 << 24;  // k, n up to 16 Mi (grid and index arithmetic stay in range)
+
+bool valid_matrix(size_t k, size_t n, size_t multiple) {
+    return k && n && k % multiple == 0 && n % multiple == 0 && k <= kMaxDim && n <= kMaxDim;
+}
+
+// Internal workspaces, one per (device, stream), grown on demand, zero-filled
+// when created and kept until process exit.
+struct InternalWs {
+    void *ptr = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_ws_mutex;
+std::map<std::pair<int, hipStream_t>, InternalWs> g_ws;
+
+exl3_status internal_workspace(size_t need, hipStream_t stream, void **out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return EXL3_HIP_ERROR;
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    InternalWs &ws = g_ws[{dev, stream}];
+    if (ws.bytes < need) {
+        if (ws.ptr) {
+            if (hipStreamSynchronize(stream) != hipSuccess) return EXL3_HIP_ERROR;
+            (void)hipFree(ws.ptr);
+            ws.ptr = nullptr;
+            ws.bytes = 0;
+        }
+        void *p = nullptr;
+        if (hipMalloc(&p, need) != hipSuccess) return EXL3_HIP_ERROR;
+        if (exl3k::launch_zero(p, need, stream) != hipSuccess) {
+            (void)hipFree(p);
+            return EXL3_HIP_ERROR;
+        }
+        ws.ptr = p;
+        ws.bytes = need;
+    }
+    *out = ws.ptr;
+    return EXL3_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+unsigned exl3_hip_version(void) { return EXL3_HIP_VERSION; }
+
+const char *exl3_hip_status_string(exl3_status s) {
+    switch (s) {
+    case EXL3_OK: return "ok";
+    case EXL3_INVAL_PARAMS: return "invalid parameters";
+    case EXL3_NO_SUPPORT: return "not supported";
+    case EXL3_WORKSPACE_TOO_SMALL: return "workspace too small";
+    case EXL3_HIP_ERROR: return "HIP runtime error";
+    }
+    return "unknown status";
+}
+
+size_t exl3_hip_gemv_max_rows(void) { return exl3k::kGemvMaxRows; }
+
+int exl3_hip_supports_mul_mat(unsigned bits, unsigned codebook, size_t k, size_t n, size_t rows, exl3_dtype xt,
+                              exl3_dtype yt) {
+    return valid_rate(bits, codebook) && valid_matrix(k, n, 128) && rows >= 1 && rows <= kMaxRows &&
+           valid_dtype(xt) && valid_dtype(yt);
+}
+
+size_t exl3_hip_mul_mat_workspace_bytes(size_t k, size_t n, size_t rows) {
+    if (!valid_matrix(k, n, 128) || rows < 1 || rows > kMaxRows) return 0;
+    if (rows <= (size_t)exl3k::kGemvMaxRows) return exl3k::gemv_plan(k, n, rows).bytes;
+    return exl3k::gemm_plan(k, n, rows).bytes;
+}
+
+exl3_status exl3_hip_workspace_init(void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (!workspace || !aligned(workspace, 256)) return EXL3_INVAL_PARAMS;
+    return from_hip(exl3k::launch_zero(workspace, workspace_bytes, stream));
+}
+
+exl3_status exl3_hip_mul_mat(const void *records, unsigned bits, unsigned codebook, size_t k, size_t n, const void *x,
+                             exl3_dtype xt, size_t rows, size_t x_row_stride, void *y, exl3_dtype yt,
+                             size_t y_row_stride, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (!exl3_hip_supports_mul_mat(bits, codebook, k, n, rows, xt, yt)) return EXL3_INVAL_PARAMS;
+    if (!records || !x || !y || !aligned(records, 16)) return EXL3_INVAL_PARAMS;
+    if (!aligned(x, dtype_size(xt)) || !aligned(y, dtype_size(yt))) return EXL3_INVAL_PARAMS;
+    if (x_row_stride < k || y_row_stride < n) return EXL3_INVAL_PARAMS;
+    const bool gemv = rows <= (size_t)exl3k::kGemvMaxRows;
+    const size_t need = exl3_hip_mul_mat_workspace_bytes(k, n, rows);
+    if (workspace) {
+        if (!aligned(workspace, 256)) return EXL3_INVAL_PARAMS;
+        if (workspace_bytes < need) return EXL3_WORKSPACE_TOO_SMALL;
+    } else {
+        const exl3_status st = internal_workspace(need, stream, &workspace);
+        if (st != EXL3_OK) return st;
+    }
+    const int xf = xt == EXL3_F16, yf = yt == EXL3_F16;
+    if (gemv)
+        return from_hip(exl3k::launch_gemv(records, (int)bits, (int)codebook, k, n, x, xf, rows, x_row_stride, y, yf,
+                                           y_row_stride, workspace, exl3k::gemv_plan(k, n, rows), stream));
+    return from_hip(exl3k::launch_gemm(records, (int)bits, (int)codebook, k, n, x, xf, rows, x_row_stride, y, yf,
+                                       y_row_stride, workspace, exl3k::gemm_plan(k, n, rows), stream));
+}
+
+exl3_status exl3_hip_decode(const void *src, exl3_layout layout, unsigned bits, unsigned codebook, size_t k, size_t n,
+                            size_t first_column, size_t column_count, uint16_t *out, hipStream_t stream) {
+    if (!valid_rate(bits, codebook) || !src || !out || !aligned(src, 16) || !aligned(out, 16)) return EXL3_INVAL_PARAMS;
+    const size_t mult = layout == EXL3_LAYOUT_RECORDS ? 128 : 16;
+    if (layout != EXL3_LAYOUT_RECORDS && layout != EXL3_LAYOUT_UPSTREAM_TILES) return EXL3_INVAL_PARAMS;
+    if (!valid_matrix(k, n, mult)) return EXL3_INVAL_PARAMS;
+    if (!column_count || first_column % mult || column_count % mult || first_column > n ||
+        column_count > n - first_column)
+        return EXL3_INVAL_PARAMS;
+    return from_hip(exl3k::launch_decode(src, layout == EXL3_LAYOUT_RECORDS, (int)bits, (int)codebook, k, n,
+                                         first_column, column_count, out, stream));
+}
+
+exl3_status exl3_hip_reconstruct(const void *src, exl3_layout layout, const uint16_t *su, const uint16_t *sv,
+                                 unsigned bits, unsigned codebook, size_t k, size_t n, size_t first_column,
+                                 size_t column_count, uint16_t *out, hipStream_t stream) {
+    if (!valid_rate(bits, codebook) || !src || !out || !aligned(src, 16) || !aligned(out, 2)) return EXL3_INVAL_PARAMS;
+    if (layout != EXL3_LAYOUT_RECORDS && layout != EXL3_LAYOUT_UPSTREAM_TILES) return EXL3_INVAL_PARAMS;
+    if (layout == EXL3_LAYOUT_UPSTREAM_TILES && (!su || !sv || !aligned(su, 2) || !aligned(sv, 2)))
+        return EXL3_INVAL_PARAMS;
+    if (!valid_matrix(k, n, 128)) return EXL3_INVAL_PARAMS;
+    if (!column_count || first_column % 128 || column_count % 128 || first_column > n ||
+        column_count > n - first_column)
+        return EXL3_INVAL_PARAMS;
+    return from_hip(exl3k::launch_reconstruct(src, layout == EXL3_LAYOUT_RECORDS, su, sv, (int)bits, (int)codebook, k,
+                                              n, first_column, column_count, out, stream));
+}
+
+exl3_status exl3_hip_codebook(const uint16_t *states, size_t count, unsigned codebook, uint16_t *out,
+                              hipStream_t stream) {
+    if (codebook > 2 || (count && (!states || !out))) return EXL3_INVAL_PARAMS;
+    if (!count) return EXL3_OK;
+    return from_hip(exl3k::launch_codebook(states, count, (int)codebook, out, stream));
+}
+
+exl3_status exl3_hip_hadamard128(float *values, size_t count, hipStream_t stream) {
+    if (count % 128 || (count && (!values || !aligned(values, 4)))) return EXL3_INVAL_PARAMS;
+    return from_hip(exl3k::launch_hadamard(values, count, stream));
+}
+
+exl3_status exl3_hip_pack_records(const uint16_t *packed, const uint16_t *su, const uint16_t *sv, unsigned bits,
+                                  size_t k, size_t n, void *records, hipStream_t stream) {
+    if (bits < 1 || bits > 8 || !valid_matrix(k, n, 128)) return EXL3_INVAL_PARAMS;
+    if (!packed || !su || !sv || !records) return EXL3_INVAL_PARAMS;
+    if (!aligned(packed, 16) || !aligned(su, 16) || !aligned(sv, 16) || !aligned(records, 16)) return EXL3_INVAL_PARAMS;
+    return from_hip(exl3k::launch_pack_records(packed, su, sv, (int)bits, k, n, records, stream));
+}
+
+exl3_status exl3_hip_validate_records(const void *records, size_t nbytes, unsigned bits, int *result,
+                                      hipStream_t stream) {
+    if (bits < 1 || bits > 8 || !result || (nbytes && !records)) return EXL3_INVAL_PARAMS;
+    const size_t gb = (size_t)2048 * bits + 512;
+    if (nbytes % gb) return EXL3_INVAL_PARAMS;
+    return from_hip(exl3k::launch_validate(records, nbytes / gb, (int)bits, result, stream));
+}
+
+}  // extern "C"

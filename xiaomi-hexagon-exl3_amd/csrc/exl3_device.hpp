@@ -1,0 +1,188 @@
+// exl3_device.hpp -- gfx950 device primitives for EXL3 trellis decode.
+//
+// Bitstream facts (src/exl3_codec.cpp:88-113, restated):
+//   * a 16x16 tile is 16*K little-endian u16 = 8*K u32 words; word i is
+//     u16[2i] | u16[2i+1] << 16 and stream bit b is bit 31 - (b % 32) of word b / 32;
+//   * the stream is cyclic (256*K bits); position p (0..255) has the state formed
+//     by the 16 stream bits ending (exclusive) at bit (p + 1) * K;
+//   * position p = 8 L + e sits at row 2 (L % 4) + (e & 1) + 8 ((e >> 1) & 1),
+//     column L / 4 + 8 ((e >> 2) & 1) of the tile.
+//
+// A "run" is the 16 consecutive positions p0 = 32 c + 16 h .. p0 + 15 (c in 0..7,
+// h in 0..1).  It covers tile columns c and c + 8 at the 8 rows
+//   h = 0: {0, 1, 8, 9, 2, 3, 10, 11}      h = 1: {4, 5, 12, 13, 6, 7, 14, 15}
+// (run index i -> e = i % 8, q = 2h + i / 8).  One lane decodes one run from the
+// 3..6 stream words that hold it, entirely in registers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace exl3dev {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+template <typename T, typename F>
+__device__ __forceinline__ T bitcast(F v) { return __builtin_bit_cast(T, v); }
+
+// ---------------------------------------------------------------- codebooks
+// src/exl3_codec.cpp:68-86.  mul1: s = byte sum of state * 0x83dcd12d,
+// w = fp16(fma(fp16(1024 + s), fp16 0x1eee, fp16 0xc931)); that fma is exact in
+// binary32, so one fp16 fma (exact product-sum, one RNE) gives the same bits.
+// mcg / 3inst: P' = (P & 0x8fff8fff) ^ 0x3b603b60, w = fp16(P'.lo) + fp16(P'.hi)
+// (exact sum, one RNE).
+template <int CB>
+__device__ __forceinline__ uint32_t trellis_hash(uint32_t s) {
+    if constexpr (CB == 2) return s * 0x83dcd12du;
+    else if constexpr (CB == 1) return s * 0xcbac1fedu;
+    else return s * 89226354u + 64248484u;
+}
+
+// two 16-bit states (upper bits of the arguments are ignored) -> packed fp16
+// pair, first state in the low half
+template <int CB>
+__device__ __forceinline__ uint32_t codebook_pair(uint32_t sa, uint32_t sb) {
+    const uint32_t pa = trellis_hash<CB>(sa & 0xffffu), pb = trellis_hash<CB>(sb & 0xffffu);
+    if constexpr (CB == 2) {
+        const uint32_t hsum = __builtin_amdgcn_sad_hi_u8(pb, 0u, __builtin_amdgcn_sad_u8(pa, 0u, 0x64006400u));
+        const h2 w = __builtin_elementwise_fma(bitcast<h2>(hsum), bitcast<h2>(0x1eee1eeeu), bitcast<h2>(0xc931c931u));
+        return bitcast<uint32_t>(w);
+    } else {
+        const uint32_t qa = (pa & 0x8fff8fffu) ^ 0x3b603b60u, qb = (pb & 0x8fff8fffu) ^ 0x3b603b60u;
+        const uint32_t lo = __builtin_amdgcn_perm(qb, qa, 0x05040100u);  // [qb.lo : qa.lo]
+        const uint32_t hi = __builtin_amdgcn_perm(qb, qa, 0x07060302u);  // [qb.hi : qa.hi]
+        return bitcast<uint32_t>(bitcast<h2>(lo) + bitcast<h2>(hi));
+    }
+}
+
+template <int CB>
+__device__ __forceinline__ uint16_t codebook_one(uint32_t s) {
+    return (uint16_t)(codebook_pair<CB>(s, s) & 0xffffu);
+}
+
+// ------------------------------------------------------------- run geometry
+// Window of a run after normalisation: it starts at bit OFF of word w[0] and
+// spans NW words.  For even K every lane's run starts K + 16 bits into the word
+// before word c*K (h = 0) or at the same offset of a later word (h = 1).  For odd
+// K the h = 1 runs start 16 bits earlier in their word; those lanes load one more
+// word and funnel-shift by 16 so all lanes share OFF.
+template <int K>
+struct RunGeo {
+    static constexpr int OFF = K + 16;
+    static constexpr int NW = (OFF + 15 * K + 16 + 31) / 32;
+    static constexpr int WORDS = 8 * K;          // u32 words per tile
+    static constexpr bool ODD = (K & 1) != 0;
+    static constexpr int NLOAD = ODD ? NW + 1 : NW;
+    // first loaded word (relative to c*K) for h = 0 and h = 1
+    static constexpr int BASE0 = ODD ? -2 : -1;
+    static constexpr int BASE1 = ODD ? (17 * K - 16) / 32 - 1 : (17 * K - 16) / 32;
+};
+
+// Byte offsets, within a tile, of the NLOAD words a run (c, h) reads.  They
+// depend only on the lane, so kernels compute them once.  Indices wrap at both
+// ends: the stream is cyclic (run c = 0, h = 0 reads the last word; for odd K
+// the extra normalisation word of run c = 7, h = 1 is word 0).
+template <int K>
+__device__ __forceinline__ void run_word_offsets(int c, int h, uint32_t (&off)[RunGeo<K>::NLOAD]) {
+    using G = RunGeo<K>;
+    const int base = c * K + (h ? G::BASE1 : G::BASE0);
+#pragma unroll
+    for (int j = 0; j < G::NLOAD; ++j) {
+        int idx = base + j;
+        idx = idx < 0 ? idx + G::WORDS : idx;
+        idx = idx >= G::WORDS ? idx - G::WORDS : idx;
+        off[j] = (uint32_t)idx * 4u;
+    }
+}
+
+// Load a run's words (tile = first byte of the tile, off from run_word_offsets
+// plus any lane-constant byte offset) and normalise them so that the window
+// starts at bit OFF of w[0] on every lane.
+template <int K>
+__device__ __forceinline__ void load_run(const uint8_t *__restrict__ tile, const uint32_t (&off)[RunGeo<K>::NLOAD],
+                                         int h, uint32_t (&w)[RunGeo<K>::NW]) {
+    using G = RunGeo<K>;
+    uint32_t v[G::NLOAD];
+#pragma unroll
+    for (int j = 0; j < G::NLOAD; ++j) v[j] = __builtin_nontemporal_load((const uint32_t *)(tile + off[j]));
+    if constexpr (G::ODD) {
+        const uint32_t sh = h ? 16u : 0u;  // alignbit(a, b, 0) == b
+#pragma unroll
+        for (int j = 0; j < G::NW; ++j) w[j] = __builtin_amdgcn_alignbit(v[j], v[j + 1], sh);
+    } else {
+#pragma unroll
+        for (int j = 0; j < G::NW; ++j) w[j] = v[j];
+    }
+}
+
+template <int K>
+__device__ __forceinline__ void load_run_words(const uint32_t *__restrict__ tile, int c, int h,
+                                               uint32_t (&w)[RunGeo<K>::NW]) {
+    uint32_t off[RunGeo<K>::NLOAD];
+    run_word_offsets<K>(c, h, off);
+    load_run<K>((const uint8_t *)tile, off, h, w);
+}
+
+// State i (0..15) of a run: 16 bits ending at window bit OFF + 16 + i*K,
+// returned in the low 16 bits (upper bits are junk).
+template <int K, int I>
+__device__ __forceinline__ uint32_t run_state(const uint32_t (&w)[RunGeo<K>::NW]) {
+    constexpr int E = RunGeo<K>::OFF + 16 + I * K;
+    constexpr int S = E - 16;
+    constexpr int J = S / 32;
+    if constexpr ((E - 1) / 32 == J) {
+        return w[J] >> (32 * (J + 1) - E);
+    } else {
+        return __builtin_amdgcn_alignbit(w[J], w[J + 1], 32 * (J + 2) - E);
+    }
+}
+
+// Decode one run into the two fp16 MFMA A-operand fragments:
+//   a1 = column c  rows R_h(0..7) as 4 packed pairs (slot 2v in the low half)
+//   a2 = column c+8 rows R_h(0..7)
+// with R_0 = {0,1,8,9,2,3,10,11}, R_1 = {4,5,12,13,6,7,14,15}.
+// Run index i -> (q' = i / 8, e = i % 8): a1 takes e < 4, slot 4 q' + e;
+// a2 takes e >= 4, slot 4 q' + e - 4.
+template <int K, int CB>
+__device__ __forceinline__ void decode_run(const uint32_t (&w)[RunGeo<K>::NW], u4 &a1, u4 &a2) {
+    a1.x = codebook_pair<CB>(run_state<K, 0>(w), run_state<K, 1>(w));
+    a1.y = codebook_pair<CB>(run_state<K, 2>(w), run_state<K, 3>(w));
+    a2.x = codebook_pair<CB>(run_state<K, 4>(w), run_state<K, 5>(w));
+    a2.y = codebook_pair<CB>(run_state<K, 6>(w), run_state<K, 7>(w));
+    a1.z = codebook_pair<CB>(run_state<K, 8>(w), run_state<K, 9>(w));
+    a1.w = codebook_pair<CB>(run_state<K, 10>(w), run_state<K, 11>(w));
+    a2.z = codebook_pair<CB>(run_state<K, 12>(w), run_state<K, 13>(w));
+    a2.w = codebook_pair<CB>(run_state<K, 14>(w), run_state<K, 15>(w));
+}
+
+// Row of run slot j (0..7) in half h: 4h + 2 (j / 4) + (j & 1) + 8 ((j >> 1) & 1)
+__device__ __forceinline__ int run_slot_row(int h, int j) {
+    return 4 * h + 2 * (j >> 2) + (j & 1) + 8 * ((j >> 1) & 1);
+}
+
+// ----------------------------------------------------------------- H128
+// 128-point natural-order Walsh-Hadamard butterflies over v[0..127] in LDS,
+// cooperatively by nthreads threads of the block (tid < nthreads), then the
+// 1/sqrt(128) scale; same stage order as src/exl3_codec.cpp:153-165.
+// The caller must __syncthreads() before (data written) -- this function ends
+// with a barrier.
+__device__ __forceinline__ void h128_lds(float *v, int rows, int stride, int tid, int nthreads) {
+    for (int step = 1; step < 128; step <<= 1) {
+        for (int t = tid; t < rows * 64; t += nthreads) {
+            const int r = t >> 6, b = t & 63;
+            const int i = ((b & ~(step - 1)) << 1) | (b & (step - 1));
+            float *row = v + r * stride;
+            const float a = row[i], c = row[i + step];
+            row[i] = a + c;
+            row[i + step] = a - c;
+        }
+        __syncthreads();
+    }
+    for (int t = tid; t < rows * 128; t += nthreads) v[(t >> 7) * stride + (t & 127)] *= 0.08838834764831844055f;
+    __syncthreads();
+}
+
+}  // namespace exl3dev

@@ -1,0 +1,773 @@
+// exl3_kernels.hip -- gfx950 kernels of the EXL3 packed-weight linear layer.
+//
+//   gemv_kernel      rows 1..8: each lane decodes 16 trellis positions of a tile
+//                    straight into an fp16 MFMA A-fragment (W^T), the activations
+//                    H128(x*su) arrive pre-split into fp16 hi/lo halves in the 16
+//                    MFMA columns, v_mfma_f32_16x16x32_f16 accumulates in fp32;
+//                    split-K partials are reduced in fixed order by the last
+//                    workgroup of each 128-column group, which applies H128 and sv.
+//   gemm_kernel      rows > 8: a workgroup decodes one 128x128 record per step into
+//                    LDS (fp16, n-major), streams a 128-row activation tile through
+//                    LDS and runs 16x16x32 f16 MFMAs, fp32 accumulation.
+//   decode_kernel    trellis tiles -> row-major fp16, bit-exact (exl3::decode_inner).
+//   reconstruct_kernel original-basis weights, bit-exact (exl3::reconstruct).
+// Reference semantics: src/exl3_codec.cpp, src/exl3-ggml.cpp:51-92.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "exl3_device.hpp"
+#include "exl3_launch.hpp"
+
+using namespace exl3dev;
+
+namespace exl3k {
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t h) { return (float)bitcast<_Float16>(h); }
+__device__ __forceinline__ uint16_t float_to_half_bits(float f) { return bitcast<uint16_t>((_Float16)f); }
+
+__device__ __forceinline__ size_t group_bytes(int bits) { return (size_t)2048 * bits + 512; }
+
+// Binary32 product rounded to binary32.  Kept opaque so the compiler cannot fuse
+// a following fp16 conversion into one v_fma_mix rounding: the reference rounds
+// to binary32 first and then to binary16 (src/exl3_codec.cpp:198-199).
+__device__ __forceinline__ float mul_rn_f32(float a, float b) {
+    float r;
+    asm("v_mul_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
+// Tile address of trellis tile (rk, cn) of a k x n matrix.
+template <int K>
+__device__ __forceinline__ const uint32_t *tile_ptr(const uint8_t *src, int records_layout, size_t k, size_t n,
+                                                    size_t rk, size_t cn) {
+    if (records_layout) {
+        const size_t nb = cn >> 3, kb = rk >> 3;
+        const size_t off = (nb * (k >> 7) + kb) * group_bytes(K) + ((rk & 7) * 8 + (cn & 7)) * 32 * K;
+        return (const uint32_t *)(src + off);
+    }
+    return (const uint32_t *)(src + (rk * (n >> 4) + cn) * 32 * K);
+}
+
+// ============================================================== codebook
+template <int CB>
+__global__ void codebook_kernel(const uint16_t *__restrict__ states, size_t count, uint16_t *__restrict__ out) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < count) out[i] = codebook_one<CB>(states[i]);
+}
+
+hipError_t launch_codebook(const uint16_t *states, size_t count, int cb, uint16_t *out, hipStream_t stream) {
+    const dim3 grid((unsigned)((count + 255) / 256)), block(256);
+    switch (cb) {
+    case 0: codebook_kernel<0><<<grid, block, 0, stream>>>(states, count, out); break;
+    case 1: codebook_kernel<1><<<grid, block, 0, stream>>>(states, count, out); break;
+    default: codebook_kernel<2><<<grid, block, 0, stream>>>(states, count, out); break;
+    }
+    return hipGetLastError();
+}
+
+// ============================================================== H128
+__global__ __launch_bounds__(64) void hadamard_kernel(float *__restrict__ values) {
+    __shared__ float v[128];
+    float *blk = values + (size_t)blockIdx.x * 128;
+    const int t = threadIdx.x;
+    v[t] = blk[t];
+    v[t + 64] = blk[t + 64];
+    __syncthreads();
+    h128_lds(v, 1, 128, t, 64);
+    blk[t] = v[t];
+    blk[t + 64] = v[t + 64];
+}
+
+hipError_t launch_hadamard(float *values, size_t count, hipStream_t stream) {
+    if (count) hadamard_kernel<<<dim3((unsigned)(count / 128)), dim3(64), 0, stream>>>(values);
+    return hipGetLastError();
+}
+
+// ============================================================== zero fill
+__global__ void zero_kernel(uint32_t *__restrict__ p, size_t words) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < words; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+hipError_t launch_zero(void *ptr, size_t bytes, hipStream_t stream) {
+    const size_t words = bytes / 4;
+    if (words) {
+        const unsigned blocks = (unsigned)((words + 255) / 256 < 4096 ? (words + 255) / 256 : 4096);
+        zero_kernel<<<dim3(blocks), dim3(256), 0, stream>>>((uint32_t *)ptr, words);
+    }
+    return hipGetLastError();
+}
+
+// ============================================================== decode
+// One workgroup: one 16-row tile row rk, 16 consecutive tile columns.
+// Lane (wave w, lane l): tile w*4 + l/16, run c = l%8, h = (l%16)/8.
+template <int K, int CB>
+__global__ __launch_bounds__(256) void decode_kernel(const uint8_t *__restrict__ src, int records_layout, size_t k,
+                                                     size_t n, size_t first_tile, size_t tile_count,
+                                                     uint16_t *__restrict__ out) {
+    constexpr int PITCH = 16 * 16 + 8;
+    __shared__ uint16_t tb[16 * PITCH];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const size_t rk = blockIdx.y;
+    const size_t t0 = (size_t)blockIdx.x * 16;  // first tile (relative to first_tile) of this workgroup
+    const int tl = wave * 4 + (lane >> 4);
+    const int c = lane & 7, h = (lane >> 3) & 1;
+    if (t0 + tl < tile_count) {
+        const uint32_t *tile = tile_ptr<K>(src, records_layout, k, n, rk, first_tile + t0 + tl);
+        uint32_t w[RunGeo<K>::NW];
+        load_run_words<K>(tile, c, h, w);
+        u4 a1, a2;
+        decode_run<K, CB>(w, a1, a2);
+        const uint32_t p1[4] = {a1.x, a1.y, a1.z, a1.w}, p2[4] = {a2.x, a2.y, a2.z, a2.w};
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int r0 = run_slot_row(h, 2 * v), r1 = run_slot_row(h, 2 * v + 1);
+            tb[r0 * PITCH + tl * 16 + c] = (uint16_t)(p1[v] & 0xffffu);
+            tb[r1 * PITCH + tl * 16 + c] = (uint16_t)(p1[v] >> 16);
+            tb[r0 * PITCH + tl * 16 + c + 8] = (uint16_t)(p2[v] & 0xffffu);
+            tb[r1 * PITCH + tl * 16 + c + 8] = (uint16_t)(p2[v] >> 16);
+        }
+    }
+    __syncthreads();
+    const size_t count = tile_count * 16;  // output row length
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int ch = tid + 256 * i;      // 16 rows x 32 chunks of 8 halves
+        const int row = ch >> 5, col8 = ch & 31;
+        const int tl2 = col8 >> 1;
+        if (t0 + tl2 < tile_count) {
+            const uint4 v = *(const uint4 *)(tb + row * PITCH + col8 * 8);
+            *(uint4 *)(out + (rk * 16 + row) * count + (t0 + tl2) * 16 + (col8 & 1) * 8) = v;
+        }
+    }
+}
+
+template <int K>
+static hipError_t launch_decode_k(const void *src, int rl, int cb, size_t k, size_t n, size_t first, size_t count,
+                                  uint16_t *out, hipStream_t stream) {
+    const size_t tiles = count / 16;
+    const dim3 grid((unsigned)((tiles + 15) / 16), (unsigned)(k / 16)), block(256);
+    const uint8_t *s = (const uint8_t *)src;
+    switch (cb) {
+    case 0: decode_kernel<K, 0><<<grid, block, 0, stream>>>(s, rl, k, n, first / 16, tiles, out); break;
+    case 1: decode_kernel<K, 1><<<grid, block, 0, stream>>>(s, rl, k, n, first / 16, tiles, out); break;
+    default: decode_kernel<K, 2><<<grid, block, 0, stream>>>(s, rl, k, n, first / 16, tiles, out); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_decode(const void *src, int rl, int bits, int cb, size_t k, size_t n, size_t first, size_t count,
+                         uint16_t *out, hipStream_t stream) {
+    switch (bits) {
+    case 1: return launch_decode_k<1>(src, rl, cb, k, n, first, count, out, stream);
+    case 2: return launch_decode_k<2>(src, rl, cb, k, n, first, count, out, stream);
+    case 3: return launch_decode_k<3>(src, rl, cb, k, n, first, count, out, stream);
+    case 4: return launch_decode_k<4>(src, rl, cb, k, n, first, count, out, stream);
+    case 5: return launch_decode_k<5>(src, rl, cb, k, n, first, count, out, stream);
+    case 6: return launch_decode_k<6>(src, rl, cb, k, n, first, count, out, stream);
+    case 7: return launch_decode_k<7>(src, rl, cb, k, n, first, count, out, stream);
+    default: return launch_decode_k<8>(src, rl, cb, k, n, first, count, out, stream);
+    }
+}
+
+// ============================================================== reconstruct
+// One workgroup per 128x128 block: decode into LDS (fp32), H128 along each row
+// (over n), then along each column (over k), then fp16((w * su) * sv) -- the
+// operation order of src/exl3_codec.cpp:184-202, so the result is bit-exact.
+template <int K, int CB>
+__global__ __launch_bounds__(256) void reconstruct_kernel(const uint8_t *__restrict__ src, int records_layout,
+                                                          const uint16_t *__restrict__ su,
+                                                          const uint16_t *__restrict__ sv, size_t k, size_t n,
+                                                          size_t first_column, size_t count,
+                                                          uint16_t *__restrict__ out) {
+    constexpr int P = 129;
+    __shared__ float blk[128 * P];
+    const int tid = threadIdx.x;
+    const size_t bc = blockIdx.x, brk = blockIdx.y;  // column block (within the slice), row block
+    const size_t cn0 = first_column / 16 + bc * 8, rk0 = brk * 8;
+#pragma unroll 1
+    for (int i = 0; i < 4; ++i) {
+        const int run = tid + 256 * i;
+        const int tile = run >> 4, rc = run & 15;
+        const int c = rc & 7, h = rc >> 3, tr = tile >> 3, tc = tile & 7;
+        const uint32_t *tp = tile_ptr<K>(src, records_layout, k, n, rk0 + tr, cn0 + tc);
+        uint32_t w[RunGeo<K>::NW];
+        load_run_words<K>(tp, c, h, w);
+        u4 a1, a2;
+        decode_run<K, CB>(w, a1, a2);
+        const uint32_t p1[4] = {a1.x, a1.y, a1.z, a1.w}, p2[4] = {a2.x, a2.y, a2.z, a2.w};
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int r0 = tr * 16 + run_slot_row(h, 2 * v), r1 = tr * 16 + run_slot_row(h, 2 * v + 1);
+            const int cc = tc * 16 + c;
+            blk[r0 * P + cc] = half_bits_to_float((uint16_t)(p1[v] & 0xffffu));
+            blk[r1 * P + cc] = half_bits_to_float((uint16_t)(p1[v] >> 16));
+            blk[r0 * P + cc + 8] = half_bits_to_float((uint16_t)(p2[v] & 0xffffu));
+            blk[r1 * P + cc + 8] = half_bits_to_float((uint16_t)(p2[v] >> 16));
+        }
+    }
+    __syncthreads();
+    // H128 along n for each row, one thread per row, stage order of the reference
+    if (tid < 128) {
+        float *v = blk + tid * P;
+        for (int step = 1; step < 128; step <<= 1)
+            for (int b = 0; b < 64; ++b) {
+                const int i = ((b & ~(step - 1)) << 1) | (b & (step - 1));
+                const float a = v[i], c2 = v[i + step];
+                v[i] = a + c2;
+                v[i + step] = a - c2;
+            }
+        for (int i = 0; i < 128; ++i) v[i] *= 0.08838834764831844055f;
+    }
+    __syncthreads();
+    if (tid < 128) {
+        float *v = blk + tid;
+        for (int step = 1; step < 128; step <<= 1)
+            for (int b = 0; b < 64; ++b) {
+                const int i = ((b & ~(step - 1)) << 1) | (b & (step - 1));
+                const float a = v[i * P], c2 = v[(i + step) * P];
+                v[i * P] = a + c2;
+                v[(i + step) * P] = a - c2;
+            }
+        for (int i = 0; i < 128; ++i) v[i * P] *= 0.08838834764831844055f;
+    }
+    __syncthreads();
+    const size_t gcol0 = first_column + bc * 128;  // absolute column of this block
+    const uint8_t *rec = records_layout ? src + ((gcol0 >> 7) * (k >> 7) + brk) * group_bytes(K) : nullptr;
+    const uint16_t *su_b = records_layout ? (const uint16_t *)(rec + 2048 * K) : su + brk * 128;
+    const uint16_t *sv_b = records_layout ? (const uint16_t *)(rec + 2048 * K + 256) : sv + gcol0;
+    for (int e = tid; e < 128 * 128; e += 256) {
+        const int row = e >> 7, col = e & 127;
+        const float scaled = mul_rn_f32(blk[row * P + col], half_bits_to_float(su_b[row]));
+        out[(brk * 128 + row) * count + bc * 128 + col] = float_to_half_bits(mul_rn_f32(scaled, half_bits_to_float(sv_b[col])));
+    }
+}
+
+template <int K>
+static hipError_t launch_reconstruct_k(const void *src, int rl, const uint16_t *su, const uint16_t *sv, int cb,
+                                       size_t k, size_t n, size_t first, size_t count, uint16_t *out,
+                                       hipStream_t stream) {
+    const dim3 grid((unsigned)(count / 128), (unsigned)(k / 128)), block(256);
+    const uint8_t *s = (const uint8_t *)src;
+    switch (cb) {
+    case 0: reconstruct_kernel<K, 0><<<grid, block, 0, stream>>>(s, rl, su, sv, k, n, first, count, out); break;
+    case 1: reconstruct_kernel<K, 1><<<grid, block, 0, stream>>>(s, rl, su, sv, k, n, first, count, out); break;
+    default: reconstruct_kernel<K, 2><<<grid, block, 0, stream>>>(s, rl, su, sv, k, n, first, count, out); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_reconstruct(const void *src, int rl, const uint16_t *su, const uint16_t *sv, int bits, int cb,
+                              size_t k, size_t n, size_t first, size_t count, uint16_t *out, hipStream_t stream) {
+    switch (bits) {
+    case 1: return launch_reconstruct_k<1>(src, rl, su, sv, cb, k, n, first, count, out, stream);
+    case 2: return launch_reconstruct_k<2>(src, rl, su, sv, cb, k, n, first, count, out, stream);
+    case 3: return launch_reconstruct_k<3>(src, rl, su, sv, cb, k, n, first, count, out, stream);
+    case 4: return launch_reconstruct_k<4>(src, rl, su, sv, cb, k, n, first, count, out, stream);
+    case 5: return launch_reconstruct_k<5>(src, rl, su, sv, cb, k, n, first, count, out, stream);
+    case 6: return launch_reconstruct_k<6>(src, rl, su, sv, cb, k, n, first, count, out, stream);
+    case 7: return launch_reconstruct_k<7>(src, rl, su, sv, cb, k, n, first, count, out, stream);
+    default: return launch_reconstruct_k<8>(src, rl, su, sv, cb, k, n, first, count, out, stream);
+    }
+}
+
+// ============================================================== records
+// One workgroup per record (nb, kb): 64 tiles (tile (r, c) <- upstream tile
+// (8 kb + r, 8 nb + c)), then su[128 kb ..], sv[128 nb ..].
+__global__ __launch_bounds__(256) void pack_records_kernel(const uint16_t *__restrict__ packed,
+                                                           const uint16_t *__restrict__ su,
+                                                           const uint16_t *__restrict__ sv, int bits, size_t k,
+                                                           size_t n, uint8_t *__restrict__ records) {
+    const size_t kbs = k / 128, rec_id = blockIdx.x;
+    const size_t nb = rec_id / kbs, kb = rec_id - nb * kbs;
+    uint8_t *g = records + rec_id * group_bytes(bits);
+    const int tile_u4 = 2 * bits;  // 32*bits bytes per tile = 2*bits uint4
+    for (int i = threadIdx.x; i < 64 * tile_u4; i += blockDim.x) {
+        const int t = i / tile_u4, o = i - t * tile_u4;
+        const size_t up = (kb * 8 + (t >> 3)) * (n / 16) + nb * 8 + (t & 7);
+        ((uint4 *)g)[i] = ((const uint4 *)(packed + up * 16 * bits))[o];
+    }
+    if (threadIdx.x < 16) ((uint4 *)(g + 2048 * bits))[threadIdx.x] = ((const uint4 *)(su + kb * 128))[threadIdx.x];
+    else if (threadIdx.x < 32)
+        ((uint4 *)(g + 2048 * bits + 256))[threadIdx.x - 16] = ((const uint4 *)(sv + nb * 128))[threadIdx.x - 16];
+}
+
+hipError_t launch_pack_records(const uint16_t *packed, const uint16_t *su, const uint16_t *sv, int bits, size_t k,
+                               size_t n, void *records, hipStream_t stream) {
+    const size_t recs = (k / 128) * (n / 128);
+    pack_records_kernel<<<dim3((unsigned)recs), dim3(256), 0, stream>>>(packed, su, sv, bits, k, n,
+                                                                         (uint8_t *)records);
+    return hipGetLastError();
+}
+
+__global__ void set_one_kernel(int *p) { *p = 1; }
+
+// patches/llama-exl3.patch:327-338: a scale is invalid when its exponent field is all ones
+__global__ __launch_bounds__(256) void validate_kernel(const uint8_t *__restrict__ records, int bits,
+                                                       int *__restrict__ result) {
+    const uint16_t *s = (const uint16_t *)(records + (size_t)blockIdx.x * group_bytes(bits) + 2048 * bits);
+    if ((s[threadIdx.x] & 0x7c00u) == 0x7c00u) *result = 0;
+}
+
+hipError_t launch_validate(const void *records, size_t nrecords, int bits, int *result, hipStream_t stream) {
+    set_one_kernel<<<1, 1, 0, stream>>>(result);
+    if (nrecords) validate_kernel<<<dim3((unsigned)nrecords), dim3(256), 0, stream>>>((const uint8_t *)records, bits, result);
+    return hipGetLastError();
+}
+
+// ============================================================== activations
+__device__ __forceinline__ float load_x(const void *x, int x_f16, size_t stride, size_t r, size_t i) {
+    if (x_f16) return half_bits_to_float(((const uint16_t *)x)[r * stride + i]);
+    return ((const float *)x)[r * stride + i];
+}
+
+// ============================================================== GEMV
+// One launch per call.  Workgroup (nb, split s) owns slabs [u0, u1) (32 input rows
+// each) of the 128-column group nb and walks them in chunks of kChunk slabs:
+//   1. prep: xh[r] = H128(x[r] * su) in fp32 for the 128-row blocks the chunk
+//      touches (su from record (0, kb), src/exl3-ggml.cpp:60-73), split into fp16
+//      hi = rn(xh), lo = rn(xh - hi) and scattered into MFMA B fragments in LDS:
+//      slab u, lane = m + 16 g, element j; column m < 8 holds hi of row m,
+//      column m >= 8 holds lo of row m - 8 (zero for absent rows);
+//   2. wave w takes slabs u0 + w, u0 + w + 4, ...; per slab a lane decodes, for
+//      each tile-column pair tp, one run of tile (k-tile 2 (u % 4) + g / 2,
+//      n-tile 2 tp + nl / 8), c = nl % 8, h = g % 2 (nl = lane % 16, g = lane / 16)
+//      and issues two MFMAs (A = decoded W^T fragment, B = activations).  The
+//      next slab's words are loaded while the current one is decoded.
+// D^T[n][m]: lane l holds m = l % 16, n_local = 4 (l / 16) + e.  Split-K
+// partials are reduced in fixed order by the last workgroup of the column group,
+// which also applies H128 and sv (src/exl3-ggml.cpp:84-90).
+constexpr int kChunk = 16;          // slabs per activation-prep chunk
+constexpr int kPrepPitch = 129;     // LDS pitch (floats) of a prep block row
+
+template <int K>
+__device__ __forceinline__ void gemv_prep_chunk(const uint8_t *__restrict__ records, const void *__restrict__ x,
+                                                int x_f16, size_t x_stride, int rows, int ca, int cb,
+                                                float *__restrict__ scratch, uint16_t *__restrict__ frag, int tid) {
+    constexpr int NT = kGemvWaves * 64;
+    constexpr size_t GB = (size_t)2048 * K + 512;
+    const int kb_first = ca >> 2, kb_last = (cb - 1) >> 2;
+    const int nkb = kb_last - kb_first + 1;       // <= kChunk / 4 + 1
+    const int nblk = nkb * rows;                  // block b = (kb_local, r) at scratch row b
+    for (int t = tid; t < nblk * 128; t += NT) {
+        const int blk = t >> 7, i = t & 127;
+        const int kl = blk / rows, r = blk - kl * rows;
+        const int kb = kb_first + kl;
+        const uint16_t *su = (const uint16_t *)(records + (size_t)kb * GB + 2048 * K);
+        scratch[blk * kPrepPitch + i] = load_x(x, x_f16, x_stride, r, (size_t)kb * 128 + i) * half_bits_to_float(su[i]);
+    }
+    __syncthreads();
+    h128_lds(scratch, nblk, kPrepPitch, tid, NT);
+    // scatter: one (slab-row rho) item writes the 16 B-fragment halves of its k row
+    const int nitems = (cb - ca) * 32;
+    for (int t = tid; t < nitems; t += NT) {
+        const int ul = t >> 5, rho32 = t & 31;        // slab within chunk, row within slab
+        const int u = ca + ul;
+        const int kl = (u >> 2) - kb_first, rho = (u & 3) * 32 + rho32;  // row within the 128-block
+        const int kt = rho32 >> 4, r16 = rho32 & 15;
+        const int hh = (r16 >> 2) & 1;
+        const int j = (r16 & 1) | (((r16 >> 3) & 1) << 1) | (((r16 >> 1) & 1) << 2);
+        const int g = 2 * kt + hh;
+        uint16_t *dst = frag + (size_t)ul * 512 + 16 * g * 8 + j;
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            uint16_t hi = 0, lo = 0;
+            if (m < rows) {
+                const float xv = scratch[(kl * rows + m) * kPrepPitch + rho];
+                const _Float16 h16 = (_Float16)xv;
+                hi = bitcast<uint16_t>(h16);
+                lo = bitcast<uint16_t>((_Float16)(xv - (float)h16));
+            }
+            dst[m * 8] = hi;
+            dst[(m + 8) * 8] = lo;
+        }
+    }
+    __syncthreads();
+}
+
+template <int K, int CB>
+__global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
+    const uint8_t *__restrict__ records, int kbs, int nbs, int splits, int units, const void *__restrict__ x,
+    int x_f16, size_t x_stride, float *__restrict__ partials, unsigned *__restrict__ counters,
+    void *__restrict__ y, int y_f16, size_t y_stride, int rows) {
+    constexpr int NT = kGemvWaves * 64;
+    constexpr size_t GB = (size_t)2048 * K + 512;
+    constexpr int NW = RunGeo<K>::NW;
+    constexpr int SCRATCH = (kChunk / 4 + 1) * kGemvMaxRows * kPrepPitch;   // floats
+    constexpr int RED = kGemvWaves * kGemvMaxRows * 128;                     // floats
+    __shared__ __attribute__((aligned(16))) uint16_t frag[kChunk * 512];
+    __shared__ __attribute__((aligned(16))) float scratch[SCRATCH > RED ? SCRATCH : RED];
+    __shared__ int last_flag;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int s = blockIdx.x / nbs, nb = blockIdx.x - s * nbs;
+    const int u0 = (int)((long long)units * s / splits), u1 = (int)((long long)units * (s + 1) / splits);
+    const int nl = lane & 15, g = lane >> 4;
+    const int c = nl & 7, h = g & 1, ktp = g >> 1;
+    // lane-constant byte offsets: tile (k-tile ktp, n-tile nl / 8) of the slab, plus the run's words
+    uint32_t off[RunGeo<K>::NLOAD];
+    run_word_offsets<K>(c, h, off);
+#pragma unroll
+    for (int j = 0; j < RunGeo<K>::NLOAD; ++j) off[j] += (uint32_t)((8 * ktp + (nl >> 3)) * 32 * K);
+
+    f4 acc[4][2];
+#pragma unroll
+    for (int tp = 0; tp < 4; ++tp) acc[tp][0] = acc[tp][1] = (f4){0.f, 0.f, 0.f, 0.f};
+
+    const uint8_t *colgroup = records + (size_t)nb * kbs * GB;
+    auto slab_ptr = [&](int u) {  // wave-uniform: record kb = u / 4, k-tile pair 2 (u % 4)
+        return colgroup + (size_t)(u >> 2) * GB + (size_t)((u & 3) * 16) * 32 * K;
+    };
+    uint32_t wn[4][NW];
+    for (int ca = u0; ca < u1; ca += kChunk) {
+        const int cb = ca + kChunk < u1 ? ca + kChunk : u1;
+        int u = ca + wave;
+        if (u < cb) {
+#pragma unroll
+            for (int tp = 0; tp < 4; ++tp) load_run<K>(slab_ptr(u) + 2 * tp * 32 * K, off, h, wn[tp]);
+        }
+        gemv_prep_chunk<K>(records, x, x_f16, x_stride, rows, ca, cb, scratch, frag, tid);
+        for (; u < cb; u += kGemvWaves) {
+            uint32_t w[4][NW];
+#pragma unroll
+            for (int tp = 0; tp < 4; ++tp)
+#pragma unroll
+                for (int j = 0; j < NW; ++j) w[tp][j] = wn[tp][j];
+            if (u + kGemvWaves < cb) {
+#pragma unroll
+                for (int tp = 0; tp < 4; ++tp) load_run<K>(slab_ptr(u + kGemvWaves) + 2 * tp * 32 * K, off, h, wn[tp]);
+            }
+            const h8 b = *(const h8 *)(frag + (size_t)(u - ca) * 512 + lane * 8);
+#pragma unroll
+            for (int tp = 0; tp < 4; ++tp) {
+                u4 a1, a2;
+                decode_run<K, CB>(w[tp], a1, a2);
+                acc[tp][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<h8>(a1), b, acc[tp][0], 0, 0, 0);
+                acc[tp][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<h8>(a2), b, acc[tp][1], 0, 0, 0);
+            }
+        }
+        __syncthreads();  // all fragment reads of this chunk are done before the next prep
+    }
+
+    // hi + lo: MFMA column m < 8 gets column m + 8 added
+    float *red = scratch;
+    const int m = nl;
+#pragma unroll
+    for (int tp = 0; tp < 4; ++tp)
+#pragma unroll
+        for (int mf = 0; mf < 2; ++mf)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float v = acc[tp][mf][e];
+                const float o = __shfl_down(v, 8, 16);
+                if (m < rows && m < 8) {
+                    const int nloc = 4 * g + e;
+                    const int col = 16 * (2 * tp + (nloc >> 3)) + (nloc & 7) + 8 * mf;
+                    red[(wave * kGemvMaxRows + m) * 128 + col] = v + o;
+                }
+            }
+    __syncthreads();
+    float *ybuf = scratch;  // reused after the wave sums are read
+    constexpr int PER = kGemvMaxRows * 128 / NT;
+    float part[PER];
+    const int nval = rows * 128;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int t = tid + i * NT;
+        float sum = 0.f;
+        if (t < nval) {
+            const int rr = t >> 7, col = t & 127;
+#pragma unroll
+            for (int wv = 0; wv < kGemvWaves; ++wv) sum += red[(wv * kGemvMaxRows + rr) * 128 + col];
+        }
+        part[i] = sum;
+    }
+    if (splits > 1) {
+        float *mine = partials + ((size_t)nb * splits + s) * (size_t)nval;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int t = tid + i * NT;
+            if (t < nval) mine[t] = part[i];
+        }
+        __threadfence();
+        __syncthreads();
+        if (tid == 0) last_flag = atomicAdd(counters + nb, 1u) == (unsigned)(splits - 1);
+        __syncthreads();
+        if (!last_flag) return;
+        __threadfence();
+        const float *all = partials + (size_t)nb * splits * (size_t)nval;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int t = tid + i * NT;
+            float sum = 0.f;
+            if (t < nval)
+                for (int sp = 0; sp < splits; ++sp) sum += __builtin_nontemporal_load(all + (size_t)sp * nval + t);
+            part[i] = sum;
+        }
+        if (tid == 0) atomicExch(counters + nb, 0u);  // self-reset for the next call
+    } else {
+        __syncthreads();  // every wave has read red before ybuf overwrites it
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int t = tid + i * NT;
+        if (t < nval) ybuf[(t >> 7) * 129 + (t & 127)] = part[i];
+    }
+    __syncthreads();
+    h128_lds(ybuf, rows, 129, tid, NT);
+    const uint16_t *sv = (const uint16_t *)(records + (size_t)nb * kbs * GB + 2048 * K + 256);
+    for (int t = tid; t < nval; t += NT) {
+        const int rr = t >> 7, col = t & 127;
+        const float v = ybuf[rr * 129 + col] * half_bits_to_float(sv[col]);
+        const size_t o = (size_t)rr * y_stride + (size_t)nb * 128 + col;
+        if (y_f16) ((uint16_t *)y)[o] = float_to_half_bits(v);
+        else ((float *)y)[o] = v;
+    }
+}
+
+GemvPlan gemv_plan(size_t k, size_t n, size_t rows) {
+    GemvPlan p{};
+    p.nbs = (int)(n / 128);
+    p.kbs = (int)(k / 128);
+    p.units = (int)(k / 32);
+    int s = 512 / (p.nbs > 0 ? p.nbs : 1);
+    const int smax = p.units / 8 > 0 ? p.units / 8 : 1;
+    s = s < 1 ? 1 : (s > smax ? smax : s);
+    p.splits = s;
+    size_t off = 0;
+    p.counters_off = off;
+    off += ((size_t)p.nbs * 4 + 255) & ~(size_t)255;
+    p.xprep_off = off;  // unused: activations are prepared in LDS by the GEMV kernel
+    p.partials_off = off;
+    if (s > 1) off += (size_t)p.nbs * s * rows * 128 * 4;
+    p.bytes = (off + 255) & ~(size_t)255;
+    return p;
+}
+
+template <int K>
+static hipError_t launch_gemv_k(const void *records, int cb, const void *x, int x_f16, size_t rows, size_t x_stride,
+                                void *y, int y_f16, size_t y_stride, uint8_t *ws, const GemvPlan &p,
+                                hipStream_t stream) {
+    const uint8_t *rec = (const uint8_t *)records;
+    const dim3 grid((unsigned)(p.nbs * p.splits)), block(kGemvWaves * 64);
+    float *part = (float *)(ws + p.partials_off);
+    unsigned *cnt = (unsigned *)(ws + p.counters_off);
+    switch (cb) {
+    case 0: gemv_kernel<K, 0><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.splits, p.units, x, x_f16, x_stride, part, cnt, y, y_f16, y_stride, (int)rows); break;
+    case 1: gemv_kernel<K, 1><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.splits, p.units, x, x_f16, x_stride, part, cnt, y, y_f16, y_stride, (int)rows); break;
+    default: gemv_kernel<K, 2><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.splits, p.units, x, x_f16, x_stride, part, cnt, y, y_f16, y_stride, (int)rows); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv(const void *records, int bits, int cb, size_t k, size_t n, const void *x, int x_f16,
+                       size_t rows, size_t x_stride, void *y, int y_f16, size_t y_stride, void *workspace,
+                       const GemvPlan &p, hipStream_t stream) {
+    (void)k;
+    (void)n;
+    uint8_t *ws = (uint8_t *)workspace;
+    switch (bits) {
+    case 1: return launch_gemv_k<1>(records, cb, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
+    case 2: return launch_gemv_k<2>(records, cb, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
+    case 3: return launch_gemv_k<3>(records, cb, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
+    case 4: return launch_gemv_k<4>(records, cb, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
+    case 5: return launch_gemv_k<5>(records, cb, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
+    case 6: return launch_gemv_k<6>(records, cb, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
+    case 7: return launch_gemv_k<7>(records, cb, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
+    default: return launch_gemv_k<8>(records, cb, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
+    }
+}
+
+// ============================================================== GEMM
+// Activation prep for the GEMM: xh16[r][i] = fp16(H128(x[r] * su)[i]), rows padded
+// to a multiple of 128 with zeros.  Grid (kbs, mtiles*16), 128 threads, 8 rows each.
+__global__ __launch_bounds__(128) void gemm_xprep_kernel(const uint8_t *__restrict__ records, int bits,
+                                                         const void *__restrict__ x, int x_f16, size_t x_stride,
+                                                         int rows, size_t k, uint16_t *__restrict__ xh16) {
+    __shared__ float v[8 * 129];
+    const int kb = blockIdx.x, t = threadIdx.x, r0 = blockIdx.y * 8;
+    const uint16_t *su = (const uint16_t *)(records + (size_t)kb * group_bytes(bits) + 2048 * bits);
+    const float s = half_bits_to_float(su[t]);
+    for (int r = 0; r < 8; ++r)
+        v[r * 129 + t] = (r0 + r < rows) ? load_x(x, x_f16, x_stride, r0 + r, (size_t)kb * 128 + t) * s : 0.f;
+    __syncthreads();
+    h128_lds(v, 8, 129, t, 128);
+    for (int r = 0; r < 8; ++r) xh16[(size_t)(r0 + r) * k + (size_t)kb * 128 + t] = float_to_half_bits(v[r * 129 + t]);
+}
+
+// Workgroup (m-tile mt, column group nb, split s): rows [128 mt, +128) x columns
+// [128 nb, +128), records kb in [kb0, kb1).  4 waves in a 2 x 2 grid, each
+// 64 x 64 = 4 x 4 MFMA blocks.  Per record: x tile -> LDS (row-major), record
+// decoded -> LDS n-major (Ws[n][k]), 4 k-steps of 16x16x32 MFMAs.
+template <int K, int CB>
+__global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
+    const uint8_t *__restrict__ records, int kbs, int nbs, int mtiles, int splits, const uint16_t *__restrict__ xh16,
+    size_t k, float *__restrict__ partials, unsigned *__restrict__ counters, void *__restrict__ y, int y_f16,
+    size_t y_stride, int rows) {
+    constexpr int NT = kGemmWaves * 64;
+    constexpr int XP = 128 + 8;   // LDS pitch (halves) of the activation and weight tiles
+    constexpr int OP = 128 + 4;   // LDS pitch (floats) of the output tile
+    constexpr size_t GB = (size_t)2048 * K + 512;
+    constexpr int LDS_BYTES = (2 * 128 * XP * 2) > (128 * OP * 4) ? (2 * 128 * XP * 2) : (128 * OP * 4);
+    __shared__ __attribute__((aligned(16))) uint8_t smem[LDS_BYTES];
+    __shared__ int last_flag;
+    uint16_t *Xs = (uint16_t *)smem;
+    uint16_t *Ws = Xs + 128 * XP;
+    float *Os = (float *)smem;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    int bid = blockIdx.x;
+    const int s = bid % splits;
+    bid /= splits;
+    const int nb = bid % nbs, mt = bid / nbs;
+    const int kb0 = (int)((long long)kbs * s / splits), kb1 = (int)((long long)kbs * (s + 1) / splits);
+
+    f4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = (f4){0.f, 0.f, 0.f, 0.f};
+
+    const uint16_t *xbase = xh16 + (size_t)mt * 128 * k;
+    for (int kb = kb0; kb < kb1; ++kb) {
+        // activation tile 128 x 128 fp16: 2048 uint4, 8 per thread
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int ch = tid + i * NT;
+            const int row = ch >> 4, c8 = ch & 15;
+            *(uint4 *)(Xs + row * XP + c8 * 8) = *(const uint4 *)(xbase + (size_t)row * k + (size_t)kb * 128 + c8 * 8);
+        }
+        // decode the record: 1024 runs, 4 per thread, into Ws[n][k]
+        const uint8_t *rec = records + ((size_t)nb * kbs + kb) * GB;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int run = tid + i * NT;
+            const int tile = run >> 4, rc = run & 15;
+            const int c = rc & 7, h = rc >> 3, tr = tile >> 3, tc = tile & 7;
+            uint32_t w[RunGeo<K>::NW];
+            load_run_words<K>((const uint32_t *)(rec + (8 * tr + tc) * 32 * K), c, h, w);
+            u4 a1, a2;
+            decode_run<K, CB>(w, a1, a2);
+            const uint32_t p1[4] = {a1.x, a1.y, a1.z, a1.w}, p2[4] = {a2.x, a2.y, a2.z, a2.w};
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int kr = tr * 16 + run_slot_row(h, 2 * v);  // even row; pair = rows kr, kr + 1
+                *(uint32_t *)(Ws + (tc * 16 + c) * XP + kr) = p1[v];
+                *(uint32_t *)(Ws + (tc * 16 + c + 8) * XP + kr) = p2[v];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            h8 a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                a[i] = *(const h8 *)(Xs + (wm * 64 + i * 16 + (lane & 15)) * XP + ks * 32 + 8 * (lane >> 4));
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                b[j] = *(const h8 *)(Ws + (wn * 64 + j * 16 + (lane & 15)) * XP + ks * 32 + 8 * (lane >> 4));
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+    // D[m][n]: lane l holds n = l % 16, m = 4 (l / 16) + e
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                Os[(wm * 64 + i * 16 + 4 * (lane >> 4) + e) * OP + wn * 64 + j * 16 + (lane & 15)] = acc[i][j][e];
+    __syncthreads();
+    const int row0 = mt * 128;
+    const int vrows = rows - row0 < 128 ? rows - row0 : 128;
+    if (splits > 1) {
+        float *mine = partials + (((size_t)mt * nbs + nb) * splits + s) * 128 * 128;
+        for (int t = tid; t < vrows * 128; t += NT) mine[t] = Os[(t >> 7) * OP + (t & 127)];
+        __threadfence();
+        __syncthreads();
+        if (tid == 0) last_flag = atomicAdd(counters + (size_t)mt * nbs + nb, 1u) == (unsigned)(splits - 1);
+        __syncthreads();
+        if (!last_flag) return;
+        __threadfence();
+        const float *all = partials + ((size_t)mt * nbs + nb) * splits * 128 * 128;
+        for (int t = tid; t < vrows * 128; t += NT) {
+            float sum = 0.f;
+            for (int sp = 0; sp < splits; ++sp) sum += __builtin_nontemporal_load(all + (size_t)sp * 128 * 128 + t);
+            Os[(t >> 7) * OP + (t & 127)] = sum;
+        }
+        if (tid == 0) atomicExch(counters + (size_t)mt * nbs + nb, 0u);
+        __syncthreads();
+    }
+    h128_lds(Os, vrows, OP, tid, NT);
+    const uint16_t *sv = (const uint16_t *)(records + (size_t)nb * kbs * GB + 2048 * K + 256);
+    for (int t = tid; t < vrows * 128; t += NT) {
+        const int rr = t >> 7, col = t & 127;
+        const float v = Os[rr * OP + col] * half_bits_to_float(sv[col]);
+        const size_t o = (size_t)(row0 + rr) * y_stride + (size_t)nb * 128 + col;
+        if (y_f16) ((uint16_t *)y)[o] = float_to_half_bits(v);
+        else ((float *)y)[o] = v;
+    }
+}
+
+GemmPlan gemm_plan(size_t k, size_t n, size_t rows) {
+    GemmPlan p{};
+    p.nbs = (int)(n / 128);
+    p.kbs = (int)(k / 128);
+    p.mtiles = (int)((rows + 127) / 128);
+    const int tiles = p.nbs * p.mtiles;
+    int s = (512 + tiles - 1) / tiles;
+    const int smax = p.kbs / 4 > 0 ? p.kbs / 4 : 1;
+    s = s < 1 ? 1 : (s > smax ? smax : s);
+    p.splits = s;
+    size_t off = 0;
+    p.counters_off = off;
+    off += ((size_t)tiles * 4 + 255) & ~(size_t)255;
+    p.xh_off = off;
+    off += (size_t)p.mtiles * 128 * k * 2;
+    p.partials_off = off;
+    if (s > 1) off += (size_t)tiles * s * 128 * 128 * 4;
+    p.bytes = (off + 255) & ~(size_t)255;
+    return p;
+}
+
+template <int K>
+static hipError_t launch_gemm_k(const void *records, int cb, size_t k, const void *x, int x_f16, size_t rows,
+                                size_t x_stride, void *y, int y_f16, size_t y_stride, uint8_t *ws, const GemmPlan &p,
+                                hipStream_t stream) {
+    const uint8_t *rec = (const uint8_t *)records;
+    uint16_t *xh = (uint16_t *)(ws + p.xh_off);
+    gemm_xprep_kernel<<<dim3(p.kbs, p.mtiles * 16), dim3(128), 0, stream>>>(rec, K, x, x_f16, x_stride, (int)rows, k, xh);
+    const dim3 grid((unsigned)(p.mtiles * p.nbs * p.splits)), block(kGemmWaves * 64);
+    float *part = (float *)(ws + p.partials_off);
+    unsigned *cnt = (unsigned *)(ws + p.counters_off);
+    switch (cb) {
+    case 0: gemm_kernel<K, 0><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, xh, k, part, cnt, y, y_f16, y_stride, (int)rows); break;
+    case 1: gemm_kernel<K, 1><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, xh, k, part, cnt, y, y_f16, y_stride, (int)rows); break;
+    default: gemm_kernel<K, 2><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, xh, k, part, cnt, y, y_f16, y_stride, (int)rows); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm(const void *records, int bits, int cb, size_t k, size_t n, const void *x, int x_f16,
+                       size_t rows, size_t x_stride, void *y, int y_f16, size_t y_stride, void *workspace,
+                       const GemmPlan &p, hipStream_t stream) {
+    (void)n;
+    uint8_t *ws = (uint8_t *)workspace;
+    switch (bits) {
+    case 1: return launch_gemm_k<1>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
+    case 2: return launch_gemm_k<2>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
+    case 3: return launch_gemm_k<3>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
+    case 4: return launch_gemm_k<4>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
+    case 5: return launch_gemm_k<5>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
+    case 6: return launch_gemm_k<6>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
+    case 7: return launch_gemm_k<7>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
+    default: return launch_gemm_k<8>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
+    }
+}
+
+}  // namespace exl3k

@@ -1,0 +1,47 @@
+// exl3_launch.hpp -- internal launcher interface between the C-ABI (exl3_api.cpp)
+// and the gfx950 kernels (exl3_kernels.hip).  Launchers assume the caller has
+// validated every argument; they only enqueue work and return hipGetLastError().
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace exl3k {
+
+constexpr int kGemvMaxRows = 8;   // GEMV packs hi/lo fp16 halves of up to 8 rows into 16 MFMA columns
+constexpr int kGemvWaves = 4;     // waves per GEMV workgroup
+constexpr int kGemmBM = 128;      // GEMM rows per workgroup tile
+constexpr int kGemmWaves = 4;
+
+struct GemvPlan {
+    int nbs, kbs, units, splits;  // units = k / 32 slabs
+    size_t counters_off, xprep_off, partials_off, bytes;
+};
+struct GemmPlan {
+    int nbs, kbs, mtiles, splits;
+    size_t counters_off, xh_off, partials_off, bytes;
+};
+
+GemvPlan gemv_plan(size_t k, size_t n, size_t rows);
+GemmPlan gemm_plan(size_t k, size_t n, size_t rows);
+
+hipError_t launch_gemv(const void *records, int bits, int cb, size_t k, size_t n, const void *x, int x_f16,
+                       size_t rows, size_t x_stride, void *y, int y_f16, size_t y_stride, void *workspace,
+                       const GemvPlan &plan, hipStream_t stream);
+hipError_t launch_gemm(const void *records, int bits, int cb, size_t k, size_t n, const void *x, int x_f16,
+                       size_t rows, size_t x_stride, void *y, int y_f16, size_t y_stride, void *workspace,
+                       const GemmPlan &plan, hipStream_t stream);
+hipError_t launch_decode(const void *src, int records_layout, int bits, int cb, size_t k, size_t n,
+                         size_t first, size_t count, uint16_t *out, hipStream_t stream);
+hipError_t launch_reconstruct(const void *src, int records_layout, const uint16_t *su, const uint16_t *sv,
+                              int bits, int cb, size_t k, size_t n, size_t first, size_t count, uint16_t *out,
+                              hipStream_t stream);
+hipError_t launch_codebook(const uint16_t *states, size_t count, int cb, uint16_t *out, hipStream_t stream);
+hipError_t launch_hadamard(float *values, size_t count, hipStream_t stream);
+hipError_t launch_pack_records(const uint16_t *packed, const uint16_t *su, const uint16_t *sv, int bits, size_t k,
+                               size_t n, void *records, hipStream_t stream);
+hipError_t launch_validate(const void *records, size_t nrecords, int bits, int *result, hipStream_t stream);
+hipError_t launch_zero(void *ptr, size_t bytes, hipStream_t stream);
+
+}  // namespace exl3k

@@ -1,0 +1,169 @@
+"""ctypes binding of the EXL3 HIP C-ABI (include/exl3_hip.h) for Python callers.
+
+Device buffers are torch tensors on a HIP device (torch is used for device
+memory and streams only).  Every call goes to libexl3_hip.so; if the library
+is missing the import fails -- there is no CPU fallback.
+"""
+import ctypes
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "libexl3_hip.so"
+
+OK, INVAL_PARAMS, NO_SUPPORT, WORKSPACE_TOO_SMALL, HIP_ERROR = range(5)
+F32, F16 = 0, 1
+CB_3INST, CB_MCG, CB_MUL1 = 0, 1, 2
+LAYOUT_UPSTREAM_TILES, LAYOUT_RECORDS = 0, 1
+
+EXPORTS = [
+    "exl3_hip_version", "exl3_hip_status_string", "exl3_hip_gemv_max_rows", "exl3_hip_supports_mul_mat",
+    "exl3_hip_mul_mat_workspace_bytes", "exl3_hip_workspace_init", "exl3_hip_mul_mat", "exl3_hip_decode",
+    "exl3_hip_reconstruct", "exl3_hip_codebook", "exl3_hip_hadamard128", "exl3_hip_pack_records",
+    "exl3_hip_validate_records",
+]
+
+
+class Exl3Error(RuntimeError):
+    def __init__(self, status, what):
+        self.status = status
+        super().__init__(f"{what}: status {status}")
+
+
+def load(path=LIB_PATH):
+    if not Path(path).exists():
+        raise ImportError(f"{path} is not built (run __graft_entry__.build() or make -C xiaomi-hexagon-exl3_amd)")
+    L = ctypes.CDLL(str(path))
+    vp, sz, u, i, st = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint, ctypes.c_int, ctypes.c_void_p
+    L.exl3_hip_version.restype = u
+    L.exl3_hip_version.argtypes = []
+    L.exl3_hip_status_string.restype = ctypes.c_char_p
+    L.exl3_hip_status_string.argtypes = [i]
+    L.exl3_hip_gemv_max_rows.restype = sz
+    L.exl3_hip_gemv_max_rows.argtypes = []
+    L.exl3_hip_supports_mul_mat.restype = i
+    L.exl3_hip_supports_mul_mat.argtypes = [u, u, sz, sz, sz, i, i]
+    L.exl3_hip_mul_mat_workspace_bytes.restype = sz
+    L.exl3_hip_mul_mat_workspace_bytes.argtypes = [sz, sz, sz]
+    L.exl3_hip_workspace_init.restype = i
+    L.exl3_hip_workspace_init.argtypes = [vp, sz, st]
+    L.exl3_hip_mul_mat.restype = i
+    L.exl3_hip_mul_mat.argtypes = [vp, u, u, sz, sz, vp, i, sz, sz, vp, i, sz, vp, sz, st]
+    L.exl3_hip_decode.restype = i
+    L.exl3_hip_decode.argtypes = [vp, i, u, u, sz, sz, sz, sz, vp, st]
+    L.exl3_hip_reconstruct.restype = i
+    L.exl3_hip_reconstruct.argtypes = [vp, i, vp, vp, u, u, sz, sz, sz, sz, vp, st]
+    L.exl3_hip_codebook.restype = i
+    L.exl3_hip_codebook.argtypes = [vp, sz, u, vp, st]
+    L.exl3_hip_hadamard128.restype = i
+    L.exl3_hip_hadamard128.argtypes = [vp, sz, st]
+    L.exl3_hip_pack_records.restype = i
+    L.exl3_hip_pack_records.argtypes = [vp, vp, vp, u, sz, sz, vp, st]
+    L.exl3_hip_validate_records.restype = i
+    L.exl3_hip_validate_records.argtypes = [vp, sz, u, vp, st]
+    return L
+
+
+_LIB = None
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        _LIB = load()
+    return _LIB
+
+
+def _stream(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _check(status, what):
+    if status != OK:
+        raise Exl3Error(status, what)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def workspace_bytes(k, n, rows):
+    return lib().exl3_hip_mul_mat_workspace_bytes(k, n, rows)
+
+
+def new_workspace(k, n, rows, device="cuda"):
+    import torch
+    nbytes = max(256, workspace_bytes(k, n, rows))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    _check(lib().exl3_hip_workspace_init(_ptr(ws), nbytes, _stream()), "workspace_init")
+    return ws
+
+
+def mul_mat(records, bits, k, n, x, codebook=CB_MUL1, out_dtype=None, y=None, workspace=None, stream=None):
+    """y = EXL3 linear layer applied to x ([rows, k] fp16/fp32 CUDA tensor, row stride x.stride(0))."""
+    import torch
+    assert x.dim() == 2 and x.stride(1) == 1 and x.dtype in (torch.float16, torch.float32)
+    rows = x.shape[0]
+    if y is None:
+        y = torch.empty((rows, n), dtype=out_dtype or torch.float32, device=x.device)
+    assert y.dim() == 2 and y.stride(1) == 1 and y.dtype in (torch.float16, torch.float32)
+    xt = F16 if x.dtype == torch.float16 else F32
+    yt = F16 if y.dtype == torch.float16 else F32
+    ws_ptr, ws_bytes = (None, 0) if workspace is None else (_ptr(workspace), workspace.numel())
+    _check(lib().exl3_hip_mul_mat(_ptr(records), bits, codebook, k, n, _ptr(x), xt, rows, x.stride(0), _ptr(y), yt,
+                                  y.stride(0), ws_ptr, ws_bytes, _stream(stream)), "mul_mat")
+    return y
+
+
+def decode(src, bits, k, n, codebook=CB_MUL1, layout=LAYOUT_UPSTREAM_TILES, first=0, count=None, out=None,
+           stream=None):
+    """Row-major fp16 bits (int16 tensor [k, count]) of the decoded trellis weights."""
+    import torch
+    count = n if count is None else count
+    if out is None:
+        out = torch.empty((k, count), dtype=torch.int16, device=src.device)
+    _check(lib().exl3_hip_decode(_ptr(src), layout, bits, codebook, k, n, first, count, _ptr(out), _stream(stream)),
+           "decode")
+    return out
+
+
+def reconstruct(src, bits, k, n, su=None, sv=None, codebook=CB_MUL1, layout=LAYOUT_UPSTREAM_TILES, first=0,
+                count=None, out=None, stream=None):
+    import torch
+    count = n if count is None else count
+    if out is None:
+        out = torch.empty((k, count), dtype=torch.int16, device=src.device)
+    _check(lib().exl3_hip_reconstruct(_ptr(src), layout, _ptr(su), _ptr(sv), bits, codebook, k, n, first, count,
+                                      _ptr(out), _stream(stream)), "reconstruct")
+    return out
+
+
+def codebook_values(states, codebook, out=None, stream=None):
+    import torch
+    if out is None:
+        out = torch.empty_like(states)
+    _check(lib().exl3_hip_codebook(_ptr(states), states.numel(), codebook, _ptr(out), _stream(stream)), "codebook")
+    return out
+
+
+def hadamard128(values, stream=None):
+    _check(lib().exl3_hip_hadamard128(_ptr(values), values.numel(), _stream(stream)), "hadamard128")
+    return values
+
+
+def pack_records(packed, su, sv, bits, k, n, out=None, stream=None):
+    import torch
+    if out is None:
+        out = torch.empty(((n // 128) * (k // 128) * (2048 * bits + 512),), dtype=torch.uint8, device=packed.device)
+    _check(lib().exl3_hip_pack_records(_ptr(packed), _ptr(su), _ptr(sv), bits, k, n, _ptr(out), _stream(stream)),
+           "pack_records")
+    return out
+
+
+def validate_records(records, bits, stream=None):
+    import torch
+    res = torch.empty(1, dtype=torch.int32, device=records.device)
+    _check(lib().exl3_hip_validate_records(_ptr(records), records.numel(), bits, _ptr(res), _stream(stream)),
+           "validate_records")
+    return int(res.item())
