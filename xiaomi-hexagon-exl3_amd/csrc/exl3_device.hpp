@@ -185,4 +185,21 @@ __device__ __forceinline__ void h128_lds(float *v, int rows, int stride, int tid
     __syncthreads();
 }
 
+// H128 of one 128-block held by a wave: lane l owns element l in v0 and element
+// l + 64 in v1.  Stages 1..32 pair lanes l and l ^ step, stage 64 pairs v0/v1;
+// each butterfly is (a + b, a - b) with a the lower index, in the reference's
+// stage order (src/exl3_codec.cpp:153-165), then the 1/sqrt(128) scale.
+__device__ __forceinline__ void h128_wave(float &v0, float &v1, int lane) {
+#pragma unroll
+    for (int step = 1; step < 64; step <<= 1) {
+        const float sgn = (lane & step) ? -1.f : 1.f;  // upper element: partner - own
+        const float p0 = __shfl_xor(v0, step, 64), p1 = __shfl_xor(v1, step, 64);
+        v0 = __builtin_fmaf(v0, sgn, p0);
+        v1 = __builtin_fmaf(v1, sgn, p1);
+    }
+    const float a = v0, b = v1;
+    v0 = (a + b) * 0.08838834764831844055f;
+    v1 = (a - b) * 0.08838834764831844055f;
+}
+
 }  // namespace exl3dev

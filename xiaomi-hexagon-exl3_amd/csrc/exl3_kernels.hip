@@ -15,6 +15,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "exl3_device.hpp"
 #include "exl3_launch.hpp"
 
@@ -34,6 +36,30 @@ __device__ __forceinline__ float mul_rn_f32(float a, float b) {
     float r;
     asm("v_mul_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
     return r;
+}
+
+// Split-K partials cross XCDs (each XCD has its own L2).  They are written and
+// read with agent-scope relaxed atomics (sc1: coherent at device scope, no L2
+// write-back or invalidate of unrelated lines); the writer waits for its stores
+// to complete before the arrival counter is bumped.
+__device__ __forceinline__ void store_coherent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// returns true in every thread of the last of `total` arriving workgroups
+__device__ __forceinline__ bool arrive_last(unsigned *counter, unsigned total, int *flag_lds) {
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0)
+        *flag_lds = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == total - 1;
+    __syncthreads();
+    return *flag_lds != 0;
+}
+__device__ __forceinline__ void reset_counter(unsigned *counter) {
+    __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Tile address of trellis tile (rk, cn) of a k x n matrix.
@@ -337,121 +363,245 @@ __device__ __forceinline__ float load_x(const void *x, int x_f16, size_t stride,
 // D^T[n][m]: lane l holds m = l % 16, n_local = 4 (l / 16) + e.  Split-K
 // partials are reduced in fixed order by the last workgroup of the column group,
 // which also applies H128 and sv (src/exl3-ggml.cpp:84-90).
-constexpr int kChunk = 16;          // slabs per activation-prep chunk
-constexpr int kPrepPitch = 129;     // LDS pitch (floats) of a prep block row
-
+// Weight stream of a wave: a slab is 2 k-tiles x 8 n-tiles (512 K contiguous bytes
+// of a record); each lane loads the NLOAD words of its 4 runs straight into
+// registers, DEPTH slabs ahead (statically unrolled so every wait the compiler
+// inserts is exact).
 template <int K>
-__device__ __forceinline__ void gemv_prep_chunk(const uint8_t *__restrict__ records, const void *__restrict__ x,
-                                                int x_f16, size_t x_stride, int rows, int ca, int cb,
-                                                float *__restrict__ scratch, uint16_t *__restrict__ frag, int tid) {
-    constexpr int NT = kGemvWaves * 64;
-    constexpr size_t GB = (size_t)2048 * K + 512;
-    const int kb_first = ca >> 2, kb_last = (cb - 1) >> 2;
-    const int nkb = kb_last - kb_first + 1;       // <= kChunk / 4 + 1
-    const int nblk = nkb * rows;                  // block b = (kb_local, r) at scratch row b
-    for (int t = tid; t < nblk * 128; t += NT) {
-        const int blk = t >> 7, i = t & 127;
-        const int kl = blk / rows, r = blk - kl * rows;
-        const int kb = kb_first + kl;
-        const uint16_t *su = (const uint16_t *)(records + (size_t)kb * GB + 2048 * K);
-        scratch[blk * kPrepPitch + i] = load_x(x, x_f16, x_stride, r, (size_t)kb * 128 + i) * half_bits_to_float(su[i]);
-    }
-    __syncthreads();
-    h128_lds(scratch, nblk, kPrepPitch, tid, NT);
-    // scatter: one (slab-row rho) item writes the 16 B-fragment halves of its k row
-    const int nitems = (cb - ca) * 32;
-    for (int t = tid; t < nitems; t += NT) {
-        const int ul = t >> 5, rho32 = t & 31;        // slab within chunk, row within slab
-        const int u = ca + ul;
-        const int kl = (u >> 2) - kb_first, rho = (u & 3) * 32 + rho32;  // row within the 128-block
-        const int kt = rho32 >> 4, r16 = rho32 & 15;
-        const int hh = (r16 >> 2) & 1;
-        const int j = (r16 & 1) | (((r16 >> 3) & 1) << 1) | (((r16 >> 1) & 1) << 2);
-        const int g = 2 * kt + hh;
-        uint16_t *dst = frag + (size_t)ul * 512 + 16 * g * 8 + j;
-#pragma unroll
-        for (int m = 0; m < 8; ++m) {
-            uint16_t hi = 0, lo = 0;
-            if (m < rows) {
-                const float xv = scratch[(kl * rows + m) * kPrepPitch + rho];
-                const _Float16 h16 = (_Float16)xv;
-                hi = bitcast<uint16_t>(h16);
-                lo = bitcast<uint16_t>((_Float16)(xv - (float)h16));
-            }
-            dst[m * 8] = hi;
-            dst[(m + 8) * 8] = lo;
-        }
-    }
-    __syncthreads();
+struct GemvStream {
+    static constexpr int SLAB = 512 * K;
+    static constexpr int WORDS = 4 * RunGeo<K>::NLOAD;                   // registers per slab and lane
+    static constexpr int DEPTH = WORDS <= 12 ? 4 : (WORDS <= 16 ? 3 : 2);
+};
+constexpr int kFusedPrepRows = 2;    // rows <= this: activation prep inside the GEMV kernel
+constexpr int kMaxPrepBlocks = 8;    // (kb, row) blocks a wave prepares in the fused path
+
+// Four agent-coherent loads issued together, then one wait (relaxed atomic loads
+// are otherwise issued one round trip at a time).
+__device__ __forceinline__ float4 load4_coherent(const float *p0, const float *p1, const float *p2, const float *p3) {
+    float4 r;
+    asm volatile(
+        "global_load_dword %0, %4, off sc1\n\t"
+        "global_load_dword %1, %5, off sc1\n\t"
+        "global_load_dword %2, %6, off sc1\n\t"
+        "global_load_dword %3, %7, off sc1\n\t"
+        "s_waitcnt vmcnt(0)"
+        : "=&v"(r.x), "=&v"(r.y), "=&v"(r.z), "=&v"(r.w)
+        : "v"(p0), "v"(p1), "v"(p2), "v"(p3)
+        : "memory");
+    return r;
 }
 
-template <int K, int CB>
+// Compact B-fragment layout of a slab (128 * rows bytes): 16-byte groups
+// ((hl * rows + r) * 4 + g), hl = 0 hi / 1 lo, r = row, g = lane / 16; element j of
+// a group is k row 16 (g / 2) + R_{g % 2}(j) of the slab.  Lane l of the MFMA
+// B operand reads group (hl, r, g) with m = l % 16 -> (hl, r) = (m / 8, m % 8), or
+// a zero group when r >= rows.
+__device__ __forceinline__ int frag_elem_offset(int rho32, int hl, int r, int rows) {
+    const int kt = rho32 >> 4, r16 = rho32 & 15;
+    const int hh = (r16 >> 2) & 1;
+    const int j = (r16 & 1) | (((r16 >> 3) & 1) << 1) | (((r16 >> 1) & 1) << 2);
+    const int g = 2 * kt + hh;
+    return (((hl * rows + r) * 4 + g) * 8 + j) * 2;  // bytes
+}
+
+// Write hi/lo halves of one prepared activation (row r, k row rho32 of slab ul)
+__device__ __forceinline__ void frag_put(uint8_t *frag, int slab_bytes, int ul, int rho32, int r, int rows, float xv) {
+    const _Float16 h16 = (_Float16)xv;
+    uint8_t *base = frag + (size_t)ul * slab_bytes;
+    *(uint16_t *)(base + frag_elem_offset(rho32, 0, r, rows)) = bitcast<uint16_t>(h16);
+    *(uint16_t *)(base + frag_elem_offset(rho32, 1, r, rows)) = bitcast<uint16_t>((_Float16)(xv - (float)h16));
+}
+
+// Activation prep kernel for rows > kFusedPrepRows: one workgroup (64 threads =
+// one wave) per (128-row block kb, row r); writes the compact fragments of the
+// four slabs of block kb.  xh = H128(x[r] * su), su from record (0, kb)
+// (src/exl3-ggml.cpp:60-73).
+__global__ __launch_bounds__(64) void gemv_frag_kernel(const uint8_t *__restrict__ records, int bits,
+                                                       const void *__restrict__ x, int x_f16, size_t x_stride,
+                                                       int rows, uint8_t *__restrict__ frag) {
+    const int kb = blockIdx.x, r = blockIdx.y, lane = threadIdx.x;
+    const uint16_t *su = (const uint16_t *)(records + (size_t)kb * group_bytes(bits) + 2048 * bits);
+    float v0 = load_x(x, x_f16, x_stride, r, (size_t)kb * 128 + lane) * half_bits_to_float(su[lane]);
+    float v1 = load_x(x, x_f16, x_stride, r, (size_t)kb * 128 + lane + 64) * half_bits_to_float(su[lane + 64]);
+    h128_wave(v0, v1, lane);
+    const int slab_bytes = 128 * rows;
+    frag_put(frag, slab_bytes, kb * 4 + (lane >> 5), lane & 31, r, rows, v0);
+    frag_put(frag, slab_bytes, kb * 4 + 2 + (lane >> 5), lane & 31, r, rows, v1);
+}
+
+// GEMV.  Workgroup (nb, split s) owns slabs [u0, u1) of the 128-column group nb;
+// wave w takes slabs u0 + w, u0 + w + 4, ... and streams them through its LDS
+// ring (DEPTH slabs in flight).  Per slab a lane decodes, for each tile-column
+// pair tp, one run of tile (k-tile 2 (u % 4) + g / 2, n-tile 2 tp + nl / 8) with
+// c = nl % 8, h = g % 2 (nl = lane % 16, g = lane / 16) and issues two MFMAs
+// (A = decoded W^T fragment, B = activation fragment).  D^T[n][m]: lane l holds
+// m = l % 16, n_local = 4 (l / 16) + e.  Split-K partials are reduced in fixed
+// order by the last workgroup of the column group, which applies H128 and sv
+// (src/exl3-ggml.cpp:84-90).
+template <int K, int CB, bool FUSED>
 __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
     const uint8_t *__restrict__ records, int kbs, int nbs, int splits, int units, const void *__restrict__ x,
-    int x_f16, size_t x_stride, float *__restrict__ partials, unsigned *__restrict__ counters,
-    void *__restrict__ y, int y_f16, size_t y_stride, int rows) {
+    int x_f16, size_t x_stride, int rows, const uint8_t *__restrict__ frag_global, const uint8_t *__restrict__ dummy,
+    float *__restrict__ partials, unsigned *__restrict__ counters, void *__restrict__ y, int y_f16, size_t y_stride) {
+    using ST = GemvStream<K>;
     constexpr int NT = kGemvWaves * 64;
     constexpr size_t GB = (size_t)2048 * K + 512;
     constexpr int NW = RunGeo<K>::NW;
-    constexpr int SCRATCH = (kChunk / 4 + 1) * kGemvMaxRows * kPrepPitch;   // floats
-    constexpr int RED = kGemvWaves * kGemvMaxRows * 128;                     // floats
-    __shared__ __attribute__((aligned(16))) uint16_t frag[kChunk * 512];
-    __shared__ __attribute__((aligned(16))) float scratch[SCRATCH > RED ? SCRATCH : RED];
+    constexpr int NL = RunGeo<K>::NLOAD;
+    constexpr int D = ST::DEPTH;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ int last_flag;
+    uint8_t *zero16 = smem;            // 16 zero bytes: B fragment of absent rows
+    uint8_t *frag = smem + 16;
+    const int slab_bytes = 128 * rows;
+
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int s = blockIdx.x / nbs, nb = blockIdx.x - s * nbs;
     const int u0 = (int)((long long)units * s / splits), u1 = (int)((long long)units * (s + 1) / splits);
     const int nl = lane & 15, g = lane >> 4;
     const int c = nl & 7, h = g & 1, ktp = g >> 1;
-    // lane-constant byte offsets: tile (k-tile ktp, n-tile nl / 8) of the slab, plus the run's words
-    uint32_t off[RunGeo<K>::NLOAD];
+    const uint8_t *colgroup = records + (size_t)nb * kbs * GB;
+
+    // 1. activation inputs (issued first: their waits never cover the weight stream)
+    const int kb_first = u0 >> 2, kb_last = (u1 - 1) >> 2;
+    const int nkb = kb_last - kb_first + 1;
+    const int nblk = nkb * rows;
+    // raw bits only: converting here would make the compiler wait for these loads
+    // before the weight stream is issued
+    uint32_t px0[FUSED ? kMaxPrepBlocks : 1], px1[FUSED ? kMaxPrepBlocks : 1];
+    uint16_t ps0[FUSED ? kMaxPrepBlocks : 1], ps1[FUSED ? kMaxPrepBlocks : 1];
+    if constexpr (FUSED) {
+        // branch-free so that every load is in flight at once: blocks past nblk
+        // re-read block 0 and are discarded (fused path: rows is 1 or 2)
+        auto prep_loads = [&](auto is_f16) {
+            constexpr bool XF16 = decltype(is_f16)::value;
+#pragma unroll
+            for (int q = 0; q < kMaxPrepBlocks; ++q) {
+                const int blk = wave + q * kGemvWaves;
+                const int bc = blk < nblk ? blk : 0;
+                const int kb = kb_first + (rows == 1 ? bc : bc >> 1), r = rows == 1 ? 0 : (bc & 1);
+                const uint16_t *su = (const uint16_t *)(records + (size_t)kb * GB + 2048 * K);  // record (0, kb)
+                const size_t xi = (size_t)r * x_stride + (size_t)kb * 128 + lane;
+                if constexpr (XF16) {
+                    px0[q] = ((const uint16_t *)x)[xi];
+                    px1[q] = ((const uint16_t *)x)[xi + 64];
+                } else {
+                    px0[q] = ((const uint32_t *)x)[xi];
+                    px1[q] = ((const uint32_t *)x)[xi + 64];
+                }
+                ps0[q] = su[lane];
+                ps1[q] = su[lane + 64];
+            }
+        };
+        if (x_f16) prep_loads(std::true_type{});
+        else prep_loads(std::false_type{});
+    }
+    // output scales for the epilogue (record (nb, 0), src/exl3-ggml.cpp:84-85)
+    const uint16_t *svp = (const uint16_t *)(colgroup + 2048 * K + 256);
+    const float sv0 = half_bits_to_float(svp[lane]), sv1 = half_bits_to_float(svp[lane + 64]);
+
+    // 2. weight stream: this wave's slabs u0 + wave + 4 i, i < nw; DEPTH slabs in flight
+    uint32_t off[NL];
     run_word_offsets<K>(c, h, off);
 #pragma unroll
-    for (int j = 0; j < RunGeo<K>::NLOAD; ++j) off[j] += (uint32_t)((8 * ktp + (nl >> 3)) * 32 * K);
+    for (int j = 0; j < NL; ++j) off[j] += (uint32_t)((8 * ktp + (nl >> 3)) * 32 * K);
+    const int first_u = u0 + wave;
+    const int nw = first_u < u1 ? (u1 - first_u + kGemvWaves - 1) / kGemvWaves : 0;
+    // wave-uniform slab address: record kb = u / 4, k-tile pair 2 (u % 4); slabs past
+    // the end read a zero region of the workspace, so every issue is unconditional
+    // and the compiler's wait counts stay exact
+    auto slab_src = [&](int i) {
+        const int u = first_u + i * kGemvWaves;
+        return i < nw ? colgroup + (size_t)(u >> 2) * GB + (size_t)(u & 3) * ST::SLAB : dummy;
+    };
+    uint32_t buf[D][4][NL];
+    auto issue = [&](int i, uint32_t (&dst)[4][NL]) {
+        const uint8_t *src = slab_src(i);
+#pragma unroll
+        for (int tp = 0; tp < 4; ++tp)
+#pragma unroll
+            for (int j = 0; j < NL; ++j)
+                dst[tp][j] = __builtin_nontemporal_load((const uint32_t *)(src + off[j] + 2 * tp * 32 * K));
+    };
+#pragma unroll
+    for (int d = 0; d < D; ++d) issue(d, buf[d]);
 
+    // 3. activation fragments of slabs [u0, u1) into LDS
+    if (tid < 4) ((uint32_t *)zero16)[tid] = 0u;
+    if constexpr (FUSED) {
+#pragma unroll
+        for (int q = 0; q < kMaxPrepBlocks; ++q) {
+            const int blk = wave + q * kGemvWaves;
+            if (blk < nblk) {
+                const int kb = kb_first + (rows == 1 ? blk : blk >> 1), r = rows == 1 ? 0 : (blk & 1);
+                const float xa = x_f16 ? half_bits_to_float((uint16_t)px0[q]) : bitcast<float>(px0[q]);
+                const float xb = x_f16 ? half_bits_to_float((uint16_t)px1[q]) : bitcast<float>(px1[q]);
+                float v0 = xa * half_bits_to_float(ps0[q]), v1 = xb * half_bits_to_float(ps1[q]);
+                h128_wave(v0, v1, lane);
+                const int ua = kb * 4 + (lane >> 5), ub = kb * 4 + 2 + (lane >> 5);
+                if (ua >= u0 && ua < u1) frag_put(frag, slab_bytes, ua - u0, lane & 31, r, rows, v0);
+                if (ub >= u0 && ub < u1) frag_put(frag, slab_bytes, ub - u0, lane & 31, r, rows, v1);
+            }
+        }
+    } else {
+        const uint4 *src = (const uint4 *)(frag_global + (size_t)u0 * slab_bytes);
+        uint4 *dst = (uint4 *)frag;
+        for (int t = tid; t < (u1 - u0) * slab_bytes / 16; t += NT) dst[t] = src[t];
+    }
+    __syncthreads();
+
+    // 4. decode + MFMA
+    const int mrow = nl & 7, mhl = nl >> 3;
+    const bool bvalid = mrow < rows;
+    const int boff = bvalid ? ((mhl * rows + mrow) * 4 + g) * 16 : 0;
+    const uint8_t *bbase = bvalid ? frag : zero16;
+    const int bstride = bvalid ? slab_bytes : 0;
     f4 acc[4][2];
 #pragma unroll
     for (int tp = 0; tp < 4; ++tp) acc[tp][0] = acc[tp][1] = (f4){0.f, 0.f, 0.f, 0.f};
-
-    const uint8_t *colgroup = records + (size_t)nb * kbs * GB;
-    auto slab_ptr = [&](int u) {  // wave-uniform: record kb = u / 4, k-tile pair 2 (u % 4)
-        return colgroup + (size_t)(u >> 2) * GB + (size_t)((u & 3) * 16) * 32 * K;
-    };
-    uint32_t wn[4][NW];
-    for (int ca = u0; ca < u1; ca += kChunk) {
-        const int cb = ca + kChunk < u1 ? ca + kChunk : u1;
-        int u = ca + wave;
-        if (u < cb) {
+    auto consume = [&](int i, const uint32_t (&src)[4][NL], f4 (&ac)[4][2]) {
+        const int u = first_u + i * kGemvWaves;
+        const h8 b = *(const h8 *)(bbase + (size_t)(u - u0) * bstride + boff);
+        uint32_t w[4][NW];
 #pragma unroll
-            for (int tp = 0; tp < 4; ++tp) load_run<K>(slab_ptr(u) + 2 * tp * 32 * K, off, h, wn[tp]);
-        }
-        gemv_prep_chunk<K>(records, x, x_f16, x_stride, rows, ca, cb, scratch, frag, tid);
-        for (; u < cb; u += kGemvWaves) {
-            uint32_t w[4][NW];
+        for (int tp = 0; tp < 4; ++tp) {
+            if constexpr (RunGeo<K>::ODD) {
+                const uint32_t sh = h ? 16u : 0u;
 #pragma unroll
-            for (int tp = 0; tp < 4; ++tp)
+                for (int j = 0; j < NW; ++j) w[tp][j] = __builtin_amdgcn_alignbit(src[tp][j], src[tp][j + 1], sh);
+            } else {
 #pragma unroll
-                for (int j = 0; j < NW; ++j) w[tp][j] = wn[tp][j];
-            if (u + kGemvWaves < cb) {
-#pragma unroll
-                for (int tp = 0; tp < 4; ++tp) load_run<K>(slab_ptr(u + kGemvWaves) + 2 * tp * 32 * K, off, h, wn[tp]);
+                for (int j = 0; j < NW; ++j) w[tp][j] = src[tp][j];
             }
-            const h8 b = *(const h8 *)(frag + (size_t)(u - ca) * 512 + lane * 8);
+        }
+        return [&, b, w]() mutable {
 #pragma unroll
             for (int tp = 0; tp < 4; ++tp) {
                 u4 a1, a2;
                 decode_run<K, CB>(w[tp], a1, a2);
-                acc[tp][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<h8>(a1), b, acc[tp][0], 0, 0, 0);
-                acc[tp][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<h8>(a2), b, acc[tp][1], 0, 0, 0);
+                ac[tp][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<h8>(a1), b, ac[tp][0], 0, 0, 0);
+                ac[tp][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<h8>(a2), b, ac[tp][1], 0, 0, 0);
             }
+        };
+    };
+    int i0 = 0;
+    for (; i0 + D <= nw; i0 += D) {  // full groups: no branches between issue and use
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            auto work = consume(i0 + d, buf[d], acc);
+            issue(i0 + d + D, buf[d]);   // words are in registers; refill the slot
+            work();
         }
-        __syncthreads();  // all fragment reads of this chunk are done before the next prep
     }
+#pragma unroll
+    for (int d = 0; d < D; ++d)  // tail: fewer than D slabs, already in flight
+        if (i0 + d < nw) consume(i0 + d, buf[d], acc)();
 
-    // hi + lo: MFMA column m < 8 gets column m + 8 added
-    float *red = scratch;
-    const int m = nl;
+    // 5. epilogue: hi + lo (MFMA column m < 8 gets column m + 8), then the wave sum in LDS
+    __syncthreads();  // every wave is done with the fragments; LDS now holds the wave partials
+    float *red = (float *)smem;
 #pragma unroll
     for (int tp = 0; tp < 4; ++tp)
 #pragma unroll
@@ -460,14 +610,13 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
             for (int e = 0; e < 4; ++e) {
                 const float v = acc[tp][mf][e];
                 const float o = __shfl_down(v, 8, 16);
-                if (m < rows && m < 8) {
+                if (nl < rows && nl < 8) {
                     const int nloc = 4 * g + e;
                     const int col = 16 * (2 * tp + (nloc >> 3)) + (nloc & 7) + 8 * mf;
-                    red[(wave * kGemvMaxRows + m) * 128 + col] = v + o;
+                    red[(wave * kGemvMaxRows + nl) * 128 + col] = v + o;
                 }
             }
     __syncthreads();
-    float *ybuf = scratch;  // reused after the wave sums are read
     constexpr int PER = kGemvMaxRows * 128 / NT;
     float part[PER];
     const int nval = rows * 128;
@@ -487,41 +636,53 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int t = tid + i * NT;
-            if (t < nval) mine[t] = part[i];
+            if (t < nval) store_coherent(mine + t, part[i]);
         }
-        __threadfence();
-        __syncthreads();
-        if (tid == 0) last_flag = atomicAdd(counters + nb, 1u) == (unsigned)(splits - 1);
-        __syncthreads();
-        if (!last_flag) return;
-        __threadfence();
+        if (!arrive_last(counters + nb, (unsigned)splits, &last_flag)) return;
         const float *all = partials + (size_t)nb * splits * (size_t)nval;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int t = tid + i * NT;
             float sum = 0.f;
-            if (t < nval)
-                for (int sp = 0; sp < splits; ++sp) sum += __builtin_nontemporal_load(all + (size_t)sp * nval + t);
+            if (t < nval) {
+                const float *q = all + t;
+                int sp = 0;
+                for (; sp + 4 <= splits; sp += 4) {
+                    const float4 f = load4_coherent(q + (size_t)sp * nval, q + (size_t)(sp + 1) * nval,
+                                                    q + (size_t)(sp + 2) * nval, q + (size_t)(sp + 3) * nval);
+                    sum += f.x;
+                    sum += f.y;
+                    sum += f.z;
+                    sum += f.w;
+                }
+                for (; sp < splits; ++sp) sum += load_coherent(q + (size_t)sp * nval);
+            }
             part[i] = sum;
         }
-        if (tid == 0) atomicExch(counters + nb, 0u);  // self-reset for the next call
-    } else {
-        __syncthreads();  // every wave has read red before ybuf overwrites it
+        if (tid == 0) reset_counter(counters + nb);  // self-reset for the next call
     }
+    // 6. output H128 per row (one wave per row, registers) and sv
+    float *ybuf = red + kGemvWaves * kGemvMaxRows * 128;
+    __syncthreads();
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const int t = tid + i * NT;
-        if (t < nval) ybuf[(t >> 7) * 129 + (t & 127)] = part[i];
+        if (t < nval) ybuf[t] = part[i];
     }
     __syncthreads();
-    h128_lds(ybuf, rows, 129, tid, NT);
-    const uint16_t *sv = (const uint16_t *)(records + (size_t)nb * kbs * GB + 2048 * K + 256);
-    for (int t = tid; t < nval; t += NT) {
-        const int rr = t >> 7, col = t & 127;
-        const float v = ybuf[rr * 129 + col] * half_bits_to_float(sv[col]);
-        const size_t o = (size_t)rr * y_stride + (size_t)nb * 128 + col;
-        if (y_f16) ((uint16_t *)y)[o] = float_to_half_bits(v);
-        else ((float *)y)[o] = v;
+    for (int rr = wave; rr < rows; rr += kGemvWaves) {
+        float a0 = ybuf[rr * 128 + lane], a1 = ybuf[rr * 128 + lane + 64];
+        h128_wave(a0, a1, lane);
+        a0 *= sv0;
+        a1 *= sv1;
+        const size_t o = (size_t)rr * y_stride + (size_t)nb * 128;
+        if (y_f16) {
+            ((uint16_t *)y)[o + lane] = float_to_half_bits(a0);
+            ((uint16_t *)y)[o + lane + 64] = float_to_half_bits(a1);
+        } else {
+            ((float *)y)[o + lane] = a0;
+            ((float *)y)[o + lane + 64] = a1;
+        }
     }
 }
 
@@ -530,18 +691,57 @@ GemvPlan gemv_plan(size_t k, size_t n, size_t rows) {
     p.nbs = (int)(n / 128);
     p.kbs = (int)(k / 128);
     p.units = (int)(k / 32);
-    int s = 512 / (p.nbs > 0 ? p.nbs : 1);
-    const int smax = p.units / 8 > 0 ? p.units / 8 : 1;
+    const bool fused = rows <= (size_t)kFusedPrepRows;
+    int s = (512 + p.nbs - 1) / (p.nbs > 0 ? p.nbs : 1);
+    const int smax = p.units / 4 > 0 ? p.units / 4 : 1;
     s = s < 1 ? 1 : (s > smax ? smax : s);
+    // fused prep: a wave prepares at most kMaxPrepBlocks (kb, row) blocks;
+    // fragments of a workgroup must fit next to the ring in LDS
+    for (;;) {
+        const int uwg = (p.units + s - 1) / s;
+        const int nkb = (uwg + 3) / 4 + 1;
+        const bool ok_prep = !fused || nkb * (int)rows <= kMaxPrepBlocks * kGemvWaves;
+        const bool ok_lds = (size_t)uwg * 128 * rows <= 49152;
+        if ((ok_prep && ok_lds) || s >= smax) break;
+        ++s;
+    }
     p.splits = s;
     size_t off = 0;
     p.counters_off = off;
     off += ((size_t)p.nbs * 4 + 255) & ~(size_t)255;
-    p.xprep_off = off;  // unused: activations are prepared in LDS by the GEMV kernel
+    p.dummy_off = off;  // 4 KB of zeros read by the stream's issues past the last slab
+    off += 4096;
+    p.xprep_off = off;  // compact activation fragments (prep-kernel path)
+    if (!fused) off += ((size_t)p.units * 128 * rows + 255) & ~(size_t)255;
     p.partials_off = off;
     if (s > 1) off += (size_t)p.nbs * s * rows * 128 * 4;
     p.bytes = (off + 255) & ~(size_t)255;
     return p;
+}
+
+template <int K, int CB>
+static hipError_t launch_gemv_kc(const uint8_t *rec, const void *x, int x_f16, size_t rows, size_t x_stride, void *y,
+                                 int y_f16, size_t y_stride, uint8_t *ws, const GemvPlan &p, hipStream_t stream) {
+    const bool fused = rows <= (size_t)kFusedPrepRows;
+    const int uwg = (p.units + p.splits - 1) / p.splits;
+    const size_t frag_bytes = 16 + (size_t)uwg * 128 * rows;
+    const size_t red_bytes = (size_t)kGemvWaves * kGemvMaxRows * 128 * 4 + (size_t)kGemvMaxRows * 128 * 4;
+    size_t lds = frag_bytes > red_bytes ? frag_bytes : red_bytes;
+    lds = (lds + 15) & ~(size_t)15;
+    const dim3 grid((unsigned)(p.nbs * p.splits)), block(kGemvWaves * 64);
+    float *part = (float *)(ws + p.partials_off);
+    unsigned *cnt = (unsigned *)(ws + p.counters_off);
+    uint8_t *frag = ws + p.xprep_off;
+    const uint8_t *dummy = ws + p.dummy_off;
+    if (fused) {
+        gemv_kernel<K, CB, true><<<grid, block, lds, stream>>>(rec, p.kbs, p.nbs, p.splits, p.units, x, x_f16, x_stride,
+                                                               (int)rows, nullptr, dummy, part, cnt, y, y_f16, y_stride);
+    } else {
+        gemv_frag_kernel<<<dim3(p.kbs, (unsigned)rows), dim3(64), 0, stream>>>(rec, K, x, x_f16, x_stride, (int)rows, frag);
+        gemv_kernel<K, CB, false><<<grid, block, lds, stream>>>(rec, p.kbs, p.nbs, p.splits, p.units, x, x_f16,
+                                                                x_stride, (int)rows, frag, dummy, part, cnt, y, y_f16, y_stride);
+    }
+    return hipGetLastError();
 }
 
 template <int K>
@@ -549,15 +749,11 @@ static hipError_t launch_gemv_k(const void *records, int cb, const void *x, int 
                                 void *y, int y_f16, size_t y_stride, uint8_t *ws, const GemvPlan &p,
                                 hipStream_t stream) {
     const uint8_t *rec = (const uint8_t *)records;
-    const dim3 grid((unsigned)(p.nbs * p.splits)), block(kGemvWaves * 64);
-    float *part = (float *)(ws + p.partials_off);
-    unsigned *cnt = (unsigned *)(ws + p.counters_off);
     switch (cb) {
-    case 0: gemv_kernel<K, 0><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.splits, p.units, x, x_f16, x_stride, part, cnt, y, y_f16, y_stride, (int)rows); break;
-    case 1: gemv_kernel<K, 1><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.splits, p.units, x, x_f16, x_stride, part, cnt, y, y_f16, y_stride, (int)rows); break;
-    default: gemv_kernel<K, 2><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.splits, p.units, x, x_f16, x_stride, part, cnt, y, y_f16, y_stride, (int)rows); break;
+    case 0: return launch_gemv_kc<K, 0>(rec, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
+    case 1: return launch_gemv_kc<K, 1>(rec, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
+    default: return launch_gemv_kc<K, 2>(rec, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
     }
-    return hipGetLastError();
 }
 
 hipError_t launch_gemv(const void *records, int bits, int cb, size_t k, size_t n, const void *x, int x_f16,
@@ -687,20 +883,15 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
     const int vrows = rows - row0 < 128 ? rows - row0 : 128;
     if (splits > 1) {
         float *mine = partials + (((size_t)mt * nbs + nb) * splits + s) * 128 * 128;
-        for (int t = tid; t < vrows * 128; t += NT) mine[t] = Os[(t >> 7) * OP + (t & 127)];
-        __threadfence();
-        __syncthreads();
-        if (tid == 0) last_flag = atomicAdd(counters + (size_t)mt * nbs + nb, 1u) == (unsigned)(splits - 1);
-        __syncthreads();
-        if (!last_flag) return;
-        __threadfence();
+        for (int t = tid; t < vrows * 128; t += NT) store_coherent(mine + t, Os[(t >> 7) * OP + (t & 127)]);
+        if (!arrive_last(counters + (size_t)mt * nbs + nb, (unsigned)splits, &last_flag)) return;
         const float *all = partials + ((size_t)mt * nbs + nb) * splits * 128 * 128;
         for (int t = tid; t < vrows * 128; t += NT) {
             float sum = 0.f;
-            for (int sp = 0; sp < splits; ++sp) sum += __builtin_nontemporal_load(all + (size_t)sp * 128 * 128 + t);
+            for (int sp = 0; sp < splits; ++sp) sum += load_coherent(all + (size_t)sp * 128 * 128 + t);
             Os[(t >> 7) * OP + (t & 127)] = sum;
         }
-        if (tid == 0) atomicExch(counters + (size_t)mt * nbs + nb, 0u);
+        if (tid == 0) reset_counter(counters + (size_t)mt * nbs + nb);
         __syncthreads();
     }
     h128_lds(Os, vrows, OP, tid, NT);

@@ -16,7 +16,7 @@ constexpr int kGemmWaves = 4;
 
 struct GemvPlan {
     int nbs, kbs, units, splits;  // units = k / 32 slabs
-    size_t counters_off, xprep_off, partials_off, bytes;
+    size_t counters_off, dummy_off, xprep_off, partials_off, bytes;
 };
 struct GemmPlan {
     int nbs, kbs, mtiles, splits;
