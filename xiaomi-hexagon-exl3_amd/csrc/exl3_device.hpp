@@ -188,15 +188,34 @@ __device__ __forceinline__ void h128_lds(float *v, int rows, int stride, int tid
 // H128 of one 128-block held by a wave: lane l owns element l in v0 and element
 // l + 64 in v1.  Stages 1..32 pair lanes l and l ^ step, stage 64 pairs v0/v1;
 // each butterfly is (a + b, a - b) with a the lower index, in the reference's
-// stage order (src/exl3_codec.cpp:153-165), then the 1/sqrt(128) scale.
-__device__ __forceinline__ void h128_wave(float &v0, float &v1, int lane) {
-#pragma unroll
-    for (int step = 1; step < 64; step <<= 1) {
-        const float sgn = (lane & step) ? -1.f : 1.f;  // upper element: partner - own
-        const float p0 = __shfl_xor(v0, step, 64), p1 = __shfl_xor(v1, step, 64);
-        v0 = __builtin_fmaf(v0, sgn, p0);
-        v1 = __builtin_fmaf(v1, sgn, p1);
+// stage order (src/exl3_codec.cpp:153-165), then the 1/sqrt(128) scale.  Lane
+// exchanges use ds_swizzle (xor 1..16 inside 32-lane halves) and one ds_bpermute
+// (xor 32); each butterfly is one fma with a +-1 lane sign, exact like a +- b.
+template <int STEP>
+__device__ __forceinline__ float lane_xor(float v, int bperm_addr32) {
+    if constexpr (STEP == 32) {
+        return __int_as_float(__builtin_amdgcn_ds_bpermute(bperm_addr32, __float_as_int(v)));
+    } else {
+        return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (STEP << 10)));
     }
+}
+
+template <int STEP>
+__device__ __forceinline__ void h128_stage(float &v0, float &v1, int lane, int bperm_addr32) {
+    const float sgn = (lane & STEP) ? -1.f : 1.f;  // upper element: partner - own
+    const float p0 = lane_xor<STEP>(v0, bperm_addr32), p1 = lane_xor<STEP>(v1, bperm_addr32);
+    v0 = __builtin_fmaf(v0, sgn, p0);
+    v1 = __builtin_fmaf(v1, sgn, p1);
+}
+
+__device__ __forceinline__ void h128_wave(float &v0, float &v1, int lane) {
+    const int addr32 = (lane ^ 32) << 2;
+    h128_stage<1>(v0, v1, lane, addr32);
+    h128_stage<2>(v0, v1, lane, addr32);
+    h128_stage<4>(v0, v1, lane, addr32);
+    h128_stage<8>(v0, v1, lane, addr32);
+    h128_stage<16>(v0, v1, lane, addr32);
+    h128_stage<32>(v0, v1, lane, addr32);
     const float a = v0, b = v1;
     v0 = (a + b) * 0.08838834764831844055f;
     v1 = (a - b) * 0.08838834764831844055f;

@@ -374,7 +374,7 @@ struct GemvStream {
     static constexpr int DEPTH = WORDS <= 12 ? 4 : (WORDS <= 16 ? 3 : 2);
 };
 constexpr int kFusedPrepRows = 2;    // rows <= this: activation prep inside the GEMV kernel
-constexpr int kMaxPrepBlocks = 8;    // (kb, row) blocks a wave prepares in the fused path
+constexpr int kMaxPrepBlocks = 4;    // (kb, row) blocks a wave prepares in the fused path
 
 // Four agent-coherent loads issued together, then one wait (relaxed atomic loads
 // are otherwise issued one round trip at a time).
@@ -411,6 +411,13 @@ __device__ __forceinline__ void frag_put(uint8_t *frag, int slab_bytes, int ul, 
     uint8_t *base = frag + (size_t)ul * slab_bytes;
     *(uint16_t *)(base + frag_elem_offset(rho32, 0, r, rows)) = bitcast<uint16_t>(h16);
     *(uint16_t *)(base + frag_elem_offset(rho32, 1, r, rows)) = bitcast<uint16_t>((_Float16)(xv - (float)h16));
+}
+
+// hi half at p, lo half at p + lo_off (fragment byte offsets from frag_elem_offset)
+__device__ __forceinline__ void frag_put2(uint8_t *p, int lo_off, float xv) {
+    const _Float16 h16 = (_Float16)xv;
+    *(uint16_t *)p = bitcast<uint16_t>(h16);
+    *(uint16_t *)(p + lo_off) = bitcast<uint16_t>((_Float16)(xv - (float)h16));
 }
 
 // Activation prep kernel for rows > kFusedPrepRows: one workgroup (64 threads =
@@ -531,6 +538,7 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
     // 3. activation fragments of slabs [u0, u1) into LDS
     if (tid < 4) ((uint32_t *)zero16)[tid] = 0u;
     if constexpr (FUSED) {
+        const int lane_frag_off = frag_elem_offset(lane & 31, 0, 0, rows);
 #pragma unroll
         for (int q = 0; q < kMaxPrepBlocks; ++q) {
             const int blk = wave + q * kGemvWaves;
@@ -541,8 +549,9 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
                 float v0 = xa * half_bits_to_float(ps0[q]), v1 = xb * half_bits_to_float(ps1[q]);
                 h128_wave(v0, v1, lane);
                 const int ua = kb * 4 + (lane >> 5), ub = kb * 4 + 2 + (lane >> 5);
-                if (ua >= u0 && ua < u1) frag_put(frag, slab_bytes, ua - u0, lane & 31, r, rows, v0);
-                if (ub >= u0 && ub < u1) frag_put(frag, slab_bytes, ub - u0, lane & 31, r, rows, v1);
+                const int eo = lane_frag_off + r * 64;   // + hl * rows * 64 for the lo half
+                if (ua >= u0 && ua < u1) frag_put2(frag + (size_t)(ua - u0) * slab_bytes + eo, rows * 64, v0);
+                if (ub >= u0 && ub < u1) frag_put2(frag + (size_t)(ub - u0) * slab_bytes + eo, rows * 64, v1);
             }
         }
     } else {
@@ -561,10 +570,8 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
     f4 acc[4][2];
 #pragma unroll
     for (int tp = 0; tp < 4; ++tp) acc[tp][0] = acc[tp][1] = (f4){0.f, 0.f, 0.f, 0.f};
-    auto consume = [&](int i, const uint32_t (&src)[4][NL], f4 (&ac)[4][2]) {
-        const int u = first_u + i * kGemvWaves;
-        const h8 b = *(const h8 *)(bbase + (size_t)(u - u0) * bstride + boff);
-        uint32_t w[4][NW];
+    // words of slab i -> run windows (registers), then refill buf with slab i + D, then decode
+    auto take = [&](int i, const uint32_t (&src)[4][NL], uint32_t (&w)[4][NW]) {
 #pragma unroll
         for (int tp = 0; tp < 4; ++tp) {
             if constexpr (RunGeo<K>::ODD) {
@@ -576,28 +583,37 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
                 for (int j = 0; j < NW; ++j) w[tp][j] = src[tp][j];
             }
         }
-        return [&, b, w]() mutable {
+        (void)i;
+    };
+    auto mac = [&](int i, const uint32_t (&w)[4][NW]) {
+        const int u = first_u + i * kGemvWaves;
+        const h8 b = *(const h8 *)(bbase + (size_t)(u - u0) * bstride + boff);
 #pragma unroll
-            for (int tp = 0; tp < 4; ++tp) {
-                u4 a1, a2;
-                decode_run<K, CB>(w[tp], a1, a2);
-                ac[tp][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<h8>(a1), b, ac[tp][0], 0, 0, 0);
-                ac[tp][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<h8>(a2), b, ac[tp][1], 0, 0, 0);
-            }
-        };
+        for (int tp = 0; tp < 4; ++tp) {
+            u4 a1, a2;
+            decode_run<K, CB>(w[tp], a1, a2);
+            acc[tp][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<h8>(a1), b, acc[tp][0], 0, 0, 0);
+            acc[tp][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<h8>(a2), b, acc[tp][1], 0, 0, 0);
+        }
     };
     int i0 = 0;
     for (; i0 + D <= nw; i0 += D) {  // full groups: no branches between issue and use
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            auto work = consume(i0 + d, buf[d], acc);
+            uint32_t w[4][NW];
+            take(i0 + d, buf[d], w);
             issue(i0 + d + D, buf[d]);   // words are in registers; refill the slot
-            work();
+            mac(i0 + d, w);
         }
     }
 #pragma unroll
-    for (int d = 0; d < D; ++d)  // tail: fewer than D slabs, already in flight
-        if (i0 + d < nw) consume(i0 + d, buf[d], acc)();
+    for (int d = 0; d < D; ++d) {  // tail: fewer than D slabs, already in flight
+        if (i0 + d < nw) {
+            uint32_t w[4][NW];
+            take(i0 + d, buf[d], w);
+            mac(i0 + d, w);
+        }
+    }
 
     // 5. epilogue: hi + lo (MFMA column m < 8 gets column m + 8), then the wave sum in LDS
     __syncthreads();  // every wave is done with the fragments; LDS now holds the wave partials
@@ -609,7 +625,8 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float v = acc[tp][mf][e];
-                const float o = __shfl_down(v, 8, 16);
+                // row_shl:8 -> lane m of each 16-lane row reads lane m + 8 (the lo half)
+                const float o = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x108, 0xF, 0xF, true));
                 if (nl < rows && nl < 8) {
                     const int nloc = 4 * g + e;
                     const int col = 16 * (2 * tp + (nloc >> 3)) + (nloc & 7) + 8 * mf;
