@@ -8,9 +8,10 @@ Also measured in the same run: batch 2/4/8, a seeded 8-request admission trace
 
 Every step uses the next of 18 distinct copies of the weights (> 512 MB) so the
 256 MB Infinity Cache cannot serve repeats.  Inputs are resident in HBM before
-the timed region.  The roofline figure divides the algorithmic bytes by the
-average duration of the GEMV kernel, timed per launch with HIP events on the
-launch stream.
+the timed region.  Each timed region replays a HIP graph of back-to-back layer
+calls (one kernel each at batch <= 8), bracketed by HIP events on the replay
+stream, so the per-call time is the kernel's launch-to-launch time without
+Python launch cost; the roofline figure divides the algorithmic bytes by it.
 
 CPU baseline: the oracle's restatement of ggml_exl3_mul_mat (the reference CPU
 layer, same thread partition) on the same batch-1 layer, timed on this host.
@@ -18,8 +19,8 @@ layer, same thread partition) on the same batch-1 layer, timed on this host.
 import argparse
 import json
 import os
-import statistics
 import sys
+import statistics
 import time
 from pathlib import Path
 
@@ -43,7 +44,34 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-gemv", action="store_true", help="headline GEMV only (for profiling)")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="only time a plain device copy of COPY_BYTES (scales the HBM byte counters)")
     return ap.parse_args()
+
+
+COPY_BYTES = 64 << 20
+
+
+def calib_copy(args):
+    """Plain device-to-device copy of a known size: its FETCH_SIZE / WRITE_SIZE
+    readings per dispatch, divided into COPY_BYTES, give the factors that turn
+    those counters into HBM bytes for the GEMV."""
+    import torch
+    dev = torch.device("cuda", 0)
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.int32, device=dev).fill_(7)
+    dst = torch.empty_like(src)
+    for _ in range(args.warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(args.steps):
+        dst.copy_(src)
+    b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / args.steps
+    print(json.dumps({"calib_copy_bytes": COPY_BYTES, "us_per_copy": round(us, 2),
+                      "gbps_read_plus_write": round(2 * COPY_BYTES / (us * 1e-6) / 1e9, 1)}), flush=True)
 
 
 def main():
@@ -53,6 +81,9 @@ def main():
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
               "the EXL3 layer is not sharded across GPUs here.", file=sys.stderr)
         sys.exit(2)
+    if args.calib_copy:
+        calib_copy(args)
+        return
 
     import numpy as np
     import torch
@@ -81,66 +112,75 @@ def main():
     def call(i, rows, x):
         amd.mul_mat(copies[i % COPIES], BITS, K_IN, N_OUT, x, codebook=CB, y=ys[rows], workspace=ws[rows])
 
-    def timed(rows, x, steps, warmup):
-        for i in range(warmup):
+    def capture(rows, x):
+        """One HIP graph holding COPIES launches, one per weight copy: replays
+        measure the kernels back to back, free of Python launch cost."""
+        for i in range(2):
             call(i, rows, x)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(COPIES):
+                call(i, rows, x)
+        torch.cuda.synchronize()
+        return g
+
+    def timed(rows, x, steps, warmup):
+        """Average time of one layer call over >= steps launches (graph replays,
+        HIP events on the replay stream around the whole timed region)."""
+        g = capture(rows, x)
+        reps = max(1, -(-steps // COPIES))
+        for _ in range(max(1, -(-warmup // COPIES))):
+            g.replay()
         torch.cuda.synchronize()
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record(stream)
-        for i in range(steps):
-            call(i, rows, x)
+        for _ in range(reps):
+            g.replay()
         stop.record(stream)
         torch.cuda.synchronize()
-        total_ms = start.elapsed_time(stop)
-        # per-launch durations (one kernel per GEMV call) for the roofline
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-        for i in range(steps):
-            evs[i][0].record(stream)
-            call(i, rows, x)
-            evs[i][1].record(stream)
-        torch.cuda.synchronize()
-        per = [a.elapsed_time(b) for a, b in evs]
-        return total_ms / steps, statistics.mean(per), statistics.median(per)
+        return start.elapsed_time(stop) / (reps * COPIES), reps * COPIES
 
     # ---- headline: batch 1
-    ms1, kern1_mean, kern1_med = timed(1, xs[1], args.steps, args.warmup)
+    ms1, launches1 = timed(1, xs[1], args.steps, args.warmup)
     b1 = algo_bytes(K_IN, N_OUT, BITS, 1)
     value = b1 / (ms1 * 1e-3) / 1e9
-    achieved = b1 / (kern1_mean * 1e-3) / 1e9
+    achieved = value   # one kernel per layer call: the step time is the kernel's launch-to-launch time
 
     extra = {}
     if not args.only_gemv:
         for r in (2, 4, 8):
-            ms, km, _ = timed(r, xs[r], args.steps, args.warmup)
-            extra[f"gemv_rows{r}"] = {"gbps": round(algo_bytes(K_IN, N_OUT, BITS, r) / (ms * 1e-3) / 1e9, 1),
-                                      "kernel_us": round(km * 1e3, 2),
-                                      "frac_hbm": round(algo_bytes(K_IN, N_OUT, BITS, r) / (km * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
-        # admission trace: 8 requests, active rows uniform in 1..8 per step (seeded)
+            ms, _ = timed(r, xs[r], args.steps, args.warmup)
+            gbps = algo_bytes(K_IN, N_OUT, BITS, r) / (ms * 1e-3) / 1e9
+            extra[f"gemv_rows{r}"] = {"gbps": round(gbps, 1), "kernel_us": round(ms * 1e3, 2),
+                                      "frac_hbm": round(gbps / HBM_PEAK_GBPS, 4)}
+        # admission trace: 8 requests, active rows uniform in 1..8 per step (seeded), one graph
         trace = (synth.splitmix64(8080, args.steps) % np.uint64(8)).astype(int) + 1
-        for i in range(args.warmup):
-            r = int(trace[i % len(trace)])
-            call(i, r, xs8_slice(xs, r))
+        for i in range(8):
+            call(i, i + 1, xs8_slice(xs, i + 1))
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(args.steps):
+                call(i, int(trace[i]), xs8_slice(xs, int(trace[i])))
+        g.replay()
+        torch.cuda.synchronize()
         s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s_ev.record(stream)
-        tbytes = 0
-        for i in range(args.steps):
-            r = int(trace[i])
-            call(i, r, xs8_slice(xs, r))
-            tbytes += algo_bytes(K_IN, N_OUT, BITS, r)
+        g.replay()
         e_ev.record(stream)
         torch.cuda.synchronize()
         tms = s_ev.elapsed_time(e_ev)
+        tbytes = sum(algo_bytes(K_IN, N_OUT, BITS, int(r)) for r in trace)
         extra["gemv_admission_trace"] = {"gbps": round(tbytes / (tms * 1e-3) / 1e9, 1),
                                          "mean_rows": float(np.mean(trace)), "steps": args.steps}
         # prefill GEMM, M = 512
         gsteps = max(10, args.steps // 10)
-        msg, kmg, _ = timed(512, x512, gsteps, max(3, args.warmup // 4))
+        msg, _ = timed(512, x512, gsteps, max(3, args.warmup // 4))
         flops = 2.0 * 512 * K_IN * N_OUT
-        extra["gemm_m512"] = {"tflops": round(flops / (msg * 1e-3) / 1e12, 1),
-                              "call_us": round(kmg * 1e3, 1),
-                              "frac_mfma": round(flops / (kmg * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
+        tflops = flops / (msg * 1e-3) / 1e12
+        extra["gemm_m512"] = {"tflops": round(tflops, 1), "call_us": round(msg * 1e3, 1),
+                              "frac_mfma": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
 
     traffic = None
     tfile = ROOT / "profiles" / "traffic_gemv_k14336_n4096_b1.json"
@@ -156,7 +196,7 @@ def main():
         "value": round(value, 1),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": launches1,
         "warmup": args.warmup,
         "ms_per_step": round(ms1, 5),
         "higher_is_better": True,
@@ -169,8 +209,8 @@ def main():
                    "k": K_IN, "n": N_OUT, "bits": BITS, "rows": 1, "weight_copies": COPIES},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "kernel": "exl3k::gemv_kernel<4,2>", "kernel_us_mean": round(kern1_mean * 1e3, 3),
-                     "kernel_us_median": round(kern1_med * 1e3, 3), "algorithmic_bytes": b1},
+                     "kernel": "exl3k::gemv_kernel<4,2,true>", "kernel_us_mean": round(ms1 * 1e3, 3),
+                     "algorithmic_bytes": b1},
         "cpu_baseline": cpu,
     }
     line.update(extra)

@@ -66,10 +66,12 @@ size_t exl3_hip_gemv_max_rows(void);
 int exl3_hip_supports_mul_mat(unsigned bits, unsigned codebook, size_t k, size_t n, size_t rows,
                               exl3_dtype xt, exl3_dtype yt);
 
-/* Device workspace bytes exl3_hip_mul_mat needs for this problem.  The
- * workspace holds per-call staging and self-resetting completion counters:
- * it must be zero-filled once before its first use (exl3_hip_workspace_init)
- * and must not be shared by calls that may run concurrently. */
+/* Device workspace bytes exl3_hip_mul_mat needs for (k, n) at any row count
+ * 1..rows.  The workspace holds per-call staging and self-resetting completion
+ * counters: zero-fill it once before its first use (exl3_hip_workspace_init).
+ * One workspace serves any sequence of calls whose n agree, or all stay
+ * <= 65536, and whose k and rows it was sized for; calls that share one must
+ * not run concurrently (order them on one stream). */
 size_t exl3_hip_mul_mat_workspace_bytes(size_t k, size_t n, size_t rows);
 exl3_status exl3_hip_workspace_init(void *workspace, size_t workspace_bytes, hipStream_t stream);
 

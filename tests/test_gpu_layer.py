@@ -169,3 +169,62 @@ def test_linearity_full_size(amd):
         x2 = synth.activations(902, rows, k).astype(np.float32)
         ys = [run(amd, rec, bits, k, n, v) for v in (x1, x2, x1 + x2)]
         assert_layer_close(ys[2], ys[0] + ys[1], what=f"linearity rows={rows}")
+
+
+@pytest.mark.parametrize("rows", [1, 5, 37])
+def test_graph_replay_matches_eager(amd, oracle, rows):
+    """A HIP graph of mul_mat calls (split-K counters self-reset, no memset
+    nodes) replays bit-identically, with eager work between the replays."""
+    import torch
+    k, n, bits = 4096, 1024, 4
+    recs = [make_layer(700 + i, k, n, bits) for i in range(2)]
+    rds = [dev(r) for r in recs]
+    x = torch.from_numpy(synth.activations(710 + rows, rows, k)).cuda()
+    ws = amd.new_workspace(k, n, rows)
+    ys = [torch.empty((rows, n), dtype=torch.float32, device="cuda") for _ in range(2)]
+    eager = []
+    for i in range(2):
+        amd.mul_mat(rds[i], bits, k, n, x, y=ys[i], workspace=ws)
+        eager.append(ys[i].clone())
+    torch.cuda.synchronize()
+    for i in range(2):
+        ref = oracle.mul_mat(recs[i], bits, 2, k, n, x.cpu().numpy(), threads=THREADS)
+        assert_layer_close(eager[i].cpu().numpy(), ref, what=f"eager rows={rows} layer {i}")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(2):
+            amd.mul_mat(rds[i], bits, k, n, x, y=ys[i], workspace=ws)
+    for rep in range(4):
+        for y in ys:
+            y.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        for i in range(2):
+            assert torch.equal(ys[i], eager[i]), f"replay {rep} layer {i} rows={rows}"
+        # eager call on the same workspace between replays
+        amd.mul_mat(rds[1], bits, k, n, x, y=ys[1], workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(ys[1], eager[1])
+
+
+def test_one_workspace_serves_mixed_row_counts(amd):
+    """Calls of different row counts (GEMV and GEMM, several m-tiles) share a
+    caller workspace sized for the largest, and the internal workspace, in any
+    order: every result equals the one from a fresh workspace."""
+    import torch
+    k, n, bits = 2048, 4096, 4
+    rd = dev(make_layer(820, k, n, bits))
+    seq = [300, 100, 300, 5, 300, 1, 37, 300, 8, 129]
+    xs = {r: torch.from_numpy(synth.activations(821 + r, r, k)).cuda() for r in set(seq)}
+    fresh = {}
+    for r in set(seq):
+        ws = amd.new_workspace(k, n, r)
+        fresh[r] = amd.mul_mat(rd, bits, k, n, xs[r], workspace=ws).clone()
+    torch.cuda.synchronize()
+    shared = amd.new_workspace(k, n, max(seq))
+    for i, r in enumerate(seq):
+        y_shared = amd.mul_mat(rd, bits, k, n, xs[r], workspace=shared)
+        y_internal = amd.mul_mat(rd, bits, k, n, xs[r])
+        torch.cuda.synchronize()
+        assert torch.equal(y_shared, fresh[r]), f"caller workspace, call {i} rows={r}"
+        assert torch.equal(y_internal, fresh[r]), f"internal workspace, call {i} rows={r}"

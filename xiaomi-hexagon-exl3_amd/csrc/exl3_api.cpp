@@ -8,6 +8,8 @@
 
 #include <map>
 #include <mutex>
+#include <algorithm>
+#include <tuple>
 #include <utility>
 
 #include "exl3_launch.hpp"
@@ -28,20 +30,21 @@ bool valid_matrix(size_t k, size_t n, size_t multiple) {
     return k && n && k % multiple == 0 && n % multiple == 0 && k <= kMaxDim && n <= kMaxDim;
 }
 
-// Internal workspaces, one per (device, stream), grown on demand, zero-filled
-// when created and kept until process exit.
+// Internal workspaces, one per (device, stream, counter-region size), grown on
+// demand, zero-filled when created and kept until process exit.  Calls that
+// share one have the same counter layout (exl3k::counter_region_bytes).
 struct InternalWs {
     void *ptr = nullptr;
     size_t bytes = 0;
 };
 std::mutex g_ws_mutex;
-std::map<std::pair<int, hipStream_t>, InternalWs> g_ws;
+std::map<std::tuple<int, hipStream_t, size_t>, InternalWs> g_ws;
 
-exl3_status internal_workspace(size_t need, hipStream_t stream, void **out) {
+exl3_status internal_workspace(size_t need, size_t n, hipStream_t stream, void **out) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return EXL3_HIP_ERROR;
     std::lock_guard<std::mutex> lock(g_ws_mutex);
-    InternalWs &ws = g_ws[{dev, stream}];
+    InternalWs &ws = g_ws[std::make_tuple(dev, stream, exl3k::counter_region_bytes(n))];
     if (ws.bytes < need) {
         if (ws.ptr) {
             if (hipStreamSynchronize(stream) != hipSuccess) return EXL3_HIP_ERROR;
@@ -87,10 +90,17 @@ int exl3_hip_supports_mul_mat(unsigned bits, unsigned codebook, size_t k, size_t
            valid_dtype(xt) && valid_dtype(yt);
 }
 
+// The largest plan over every row count 1..rows, so one workspace serves all
+// smaller calls of the same (k, n) in turn (plans share the counter region).
 size_t exl3_hip_mul_mat_workspace_bytes(size_t k, size_t n, size_t rows) {
     if (!valid_matrix(k, n, 128) || rows < 1 || rows > kMaxRows) return 0;
-    if (rows <= (size_t)exl3k::kGemvMaxRows) return exl3k::gemv_plan(k, n, rows).bytes;
-    return exl3k::gemm_plan(k, n, rows).bytes;
+    size_t need = 0;
+    const size_t gemv_rows = rows < (size_t)exl3k::kGemvMaxRows ? rows : (size_t)exl3k::kGemvMaxRows;
+    for (size_t r = 1; r <= gemv_rows; ++r) need = std::max(need, exl3k::gemv_plan(k, n, r).bytes);
+    if (rows > (size_t)exl3k::kGemvMaxRows)
+        for (size_t mt = 1; mt <= (rows + exl3k::kGemmBM - 1) / exl3k::kGemmBM; ++mt)
+            need = std::max(need, exl3k::gemm_plan(k, n, std::min(rows, mt * exl3k::kGemmBM)).bytes);
+    return need;
 }
 
 exl3_status exl3_hip_workspace_init(void *workspace, size_t workspace_bytes, hipStream_t stream) {
@@ -111,7 +121,7 @@ exl3_status exl3_hip_mul_mat(const void *records, unsigned bits, unsigned codebo
         if (!aligned(workspace, 256)) return EXL3_INVAL_PARAMS;
         if (workspace_bytes < need) return EXL3_WORKSPACE_TOO_SMALL;
     } else {
-        const exl3_status st = internal_workspace(need, stream, &workspace);
+        const exl3_status st = internal_workspace(need, n, stream, &workspace);
         if (st != EXL3_OK) return st;
     }
     const int xf = xt == EXL3_F16, yf = yt == EXL3_F16;

@@ -725,8 +725,8 @@ GemvPlan gemv_plan(size_t k, size_t n, size_t rows) {
     p.splits = s;
     size_t off = 0;
     p.counters_off = off;
-    off += ((size_t)p.nbs * 4 + 255) & ~(size_t)255;
-    p.dummy_off = off;  // 4 KB of zeros read by the stream's issues past the last slab
+    off += counter_region_bytes(n);
+    p.dummy_off = off;  // 4 KB target of the stream's issues past the last slab (loaded, never used)
     off += 4096;
     p.xprep_off = off;  // compact activation fragments (prep-kernel path)
     if (!fused) off += ((size_t)p.units * 128 * rows + 255) & ~(size_t)255;
@@ -928,13 +928,14 @@ GemmPlan gemm_plan(size_t k, size_t n, size_t rows) {
     p.kbs = (int)(k / 128);
     p.mtiles = (int)((rows + 127) / 128);
     const int tiles = p.nbs * p.mtiles;
-    int s = (512 + tiles - 1) / tiles;
+    // split k only below kGemmSplitTiles tiles (then s == 1): counters stay in their region
+    int s = tiles >= (int)kGemmSplitTiles ? 1 : ((int)kGemmSplitTiles + tiles - 1) / tiles;
     const int smax = p.kbs / 4 > 0 ? p.kbs / 4 : 1;
     s = s < 1 ? 1 : (s > smax ? smax : s);
     p.splits = s;
     size_t off = 0;
     p.counters_off = off;
-    off += ((size_t)tiles * 4 + 255) & ~(size_t)255;
+    off += counter_region_bytes(n);
     p.xh_off = off;
     off += (size_t)p.mtiles * 128 * k * 2;
     p.partials_off = off;

@@ -14,6 +14,18 @@ constexpr int kGemvWaves = 4;     // waves per GEMV workgroup
 constexpr int kGemmBM = 128;      // GEMM rows per workgroup tile
 constexpr int kGemmWaves = 4;
 
+// Every plan puts its split-K arrival counters in the same leading region, so
+// one workspace serves calls of any row count (and any k) in turn: counters
+// return to zero at the end of every call, and no other region of any plan
+// overlaps them.  The GEMV counts one counter per column group; the GEMM splits
+// k only while it has fewer than kGemmSplitTiles output tiles, so it never
+// needs more counters than that.
+constexpr size_t kGemmSplitTiles = 512;
+inline size_t counter_region_bytes(size_t n) {
+    const size_t slots = n / 128 > kGemmSplitTiles ? n / 128 : kGemmSplitTiles;
+    return (slots * 4 + 255) & ~(size_t)255;
+}
+
 struct GemvPlan {
     int nbs, kbs, units, splits;  // units = k / 32 slabs
     size_t counters_off, dummy_off, xprep_off, partials_off, bytes;
