@@ -24,6 +24,7 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 
 template <typename T, typename F>
 __device__ __forceinline__ T bitcast(F v) { return __builtin_bit_cast(T, v); }
@@ -219,6 +220,71 @@ __device__ __forceinline__ void h128_wave(float &v0, float &v1, int lane) {
     const float a = v0, b = v1;
     v0 = (a + b) * 0.08838834764831844055f;
     v1 = (a - b) * 0.08838834764831844055f;
+}
+
+// The same transform with lane l owning elements 2 l (e0) and 2 l + 1 (e1): the
+// stride-1 butterfly is inside the lane, strides 2..64 pair lanes l and l ^ 1..32.
+__device__ __forceinline__ void h128_pair(float &e0, float &e1, int lane) {
+    const int addr32 = (lane ^ 32) << 2;
+    const float a = e0, b = e1;
+    e0 = a + b;
+    e1 = a - b;
+    h128_stage<1>(e0, e1, lane, addr32);
+    h128_stage<2>(e0, e1, lane, addr32);
+    h128_stage<4>(e0, e1, lane, addr32);
+    h128_stage<8>(e0, e1, lane, addr32);
+    h128_stage<16>(e0, e1, lane, addr32);
+    h128_stage<32>(e0, e1, lane, addr32);
+    e0 *= 0.08838834764831844055f;
+    e1 *= 0.08838834764831844055f;
+}
+
+// ------------------------------------------------------------- chunk decode
+// Chunk j (0..7) of a tile is its words [j K, j K + K): stream positions
+// 32 j .. 32 j + 31.  The state of position 32 j + t is the window
+// [K (t + 1) - 16, K (t + 1)) of stream bits counted from the chunk start (MSB
+// of word j K first); the first windows reach back into the previous chunk's
+// last word `prev` (chunk 7 for j = 0: the stream is cyclic,
+// src/exl3_codec.cpp:103-108).  A window inside one word is a bit field of that
+// word; a window across the boundary before word m is a bit field of
+// xb[m] = alignbit(w[m - 1], w[m], 16), which spans the 16 bits on each side.
+template <int K, int T>
+__device__ __forceinline__ uint32_t chunk_state(const uint32_t (&w)[K], const uint32_t (&xb)[K]) {
+    constexpr int a = K * (T + 1) - 16;  // window start, > -16
+    constexpr int m = a >= 0 ? a / 32 : -1;
+    if constexpr (a >= 0 && a + 16 <= 32 * (m + 1)) {
+        return (w[m] >> (32 * (m + 1) - a - 16)) & 0xffffu;
+    } else {
+        constexpr int b = 32 * (m + 1);  // boundary crossed; xb[m + 1] spans [b - 16, b + 16)
+        static_assert(m + 1 >= 0 && m + 1 < K, "window crosses an inner word boundary");
+        return (xb[m + 1] >> (b - a)) & 0xffffu;
+    }
+}
+
+// Positions 32 j + 8 q + e map to column j + 8 (e >> 2) and row
+// 2 q + (e & 1) + 8 ((e >> 1) & 1) of the tile (src/exl3_codec.cpp:109-113), so the
+// pair (8 q + 2 f, 8 q + 2 f + 1) is rows (2 q, 2 q + 1) + 8 (f & 1) of column
+// j + 8 (f >> 1).  frag[f] packs q = 0..3: an MFMA A fragment of 8 consecutive
+// rows (8 (f & 1) + 0..7) of one column, low half first.
+template <int K, int CB, int F, int Q>
+__device__ __forceinline__ uint32_t chunk_pair(const uint32_t (&w)[K], const uint32_t (&xb)[K]) {
+    return codebook_pair<CB>(chunk_state<K, 8 * Q + 2 * F>(w, xb), chunk_state<K, 8 * Q + 2 * F + 1>(w, xb));
+}
+template <int K, int CB, int F>
+__device__ __forceinline__ u4 chunk_frag(const uint32_t (&w)[K], const uint32_t (&xb)[K]) {
+    return (u4){chunk_pair<K, CB, F, 0>(w, xb), chunk_pair<K, CB, F, 1>(w, xb), chunk_pair<K, CB, F, 2>(w, xb),
+                chunk_pair<K, CB, F, 3>(w, xb)};
+}
+template <int K, int CB>
+__device__ __forceinline__ void decode_chunk(const uint32_t (&w)[K], uint32_t prev, u4 (&frag)[4]) {
+    uint32_t xb[K];
+    xb[0] = __builtin_amdgcn_alignbit(prev, w[0], 16);
+#pragma unroll
+    for (int m = 1; m < K; ++m) xb[m] = __builtin_amdgcn_alignbit(w[m - 1], w[m], 16);
+    frag[0] = chunk_frag<K, CB, 0>(w, xb);
+    frag[1] = chunk_frag<K, CB, 1>(w, xb);
+    frag[2] = chunk_frag<K, CB, 2>(w, xb);
+    frag[3] = chunk_frag<K, CB, 3>(w, xb);
 }
 
 }  // namespace exl3dev

@@ -13,6 +13,8 @@
 //   reconstruct_kernel original-basis weights, bit-exact (exl3::reconstruct).
 // Reference semantics: src/exl3_codec.cpp, src/exl3-ggml.cpp:51-92.
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 #include <stdint.h>
 
 #include <type_traits>
@@ -60,6 +62,27 @@ __device__ __forceinline__ bool arrive_last(unsigned *counter, unsigned total, i
 }
 __device__ __forceinline__ void reset_counter(unsigned *counter) {
     __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// sum_{sp < splits} q[sp * stride] in ascending sp order.  Up to 16 coherent
+// loads are in flight before the first add (the addresses past `splits` repeat
+// the last valid one and are not added), so the exchange costs one L2 round
+// trip per 16 splits rather than one per load.
+__device__ __forceinline__ float sum_splits(const float *q, int splits, size_t stride) {
+    constexpr int B = 16;
+    float sum = 0.f;
+    for (int base = 0; base < splits; base += B) {
+        float v[B];
+#pragma unroll
+        for (int j = 0; j < B; ++j) {
+            const int sp = base + j < splits ? base + j : splits - 1;
+            v[j] = load_coherent(q + (size_t)sp * stride);
+        }
+#pragma unroll
+        for (int j = 0; j < B; ++j)
+            if (base + j < splits) sum += v[j];
+    }
+    return sum;
 }
 
 // Tile address of trellis tile (rk, cn) of a k x n matrix.
@@ -348,346 +371,257 @@ __device__ __forceinline__ float load_x(const void *x, int x_f16, size_t stride,
 }
 
 // ============================================================== GEMV
-// One launch per call.  Workgroup (nb, split s) owns slabs [u0, u1) (32 input rows
-// each) of the 128-column group nb and walks them in chunks of kChunk slabs:
-//   1. prep: xh[r] = H128(x[r] * su) in fp32 for the 128-row blocks the chunk
-//      touches (su from record (0, kb), src/exl3-ggml.cpp:60-73), split into fp16
-//      hi = rn(xh), lo = rn(xh - hi) and scattered into MFMA B fragments in LDS:
-//      slab u, lane = m + 16 g, element j; column m < 8 holds hi of row m,
-//      column m >= 8 holds lo of row m - 8 (zero for absent rows);
-//   2. wave w takes slabs u0 + w, u0 + w + 4, ...; per slab a lane decodes, for
-//      each tile-column pair tp, one run of tile (k-tile 2 (u % 4) + g / 2,
-//      n-tile 2 tp + nl / 8), c = nl % 8, h = g % 2 (nl = lane % 16, g = lane / 16)
-//      and issues two MFMAs (A = decoded W^T fragment, B = activations).  The
-//      next slab's words are loaded while the current one is decoded.
-// D^T[n][m]: lane l holds m = l % 16, n_local = 4 (l / 16) + e.  Split-K
-// partials are reduced in fixed order by the last workgroup of the column group,
-// which also applies H128 and sv (src/exl3-ggml.cpp:84-90).
-// Weight stream of a wave: a slab is 2 k-tiles x 8 n-tiles (512 K contiguous bytes
-// of a record); each lane loads the NLOAD words of its 4 runs straight into
-// registers, DEPTH slabs ahead (statically unrolled so every wait the compiler
-// inserts is exact).
+// One launch per call.  Workgroup (nb, split s) owns the 128-row blocks
+// kb in [kb0, kb1) of the 128-column group nb.  A group is tile rows
+// 4 r4 .. 4 r4 + 3 x tile columns 2 c2, 2 c2 + 1 of record (nb, kb); wave w
+// owns column pair c2 = w % 4 and, with P = waves / 4, the groups
+// (kb, r4) numbered q = 2 (kb - kb0) + r4 with q % P = w / 4.
+//   1. prep: xh[r] = H128(x[r] * su) in fp32 (su from record (0, kb),
+//      src/exl3-ggml.cpp:60-73) for every (kb, r) of the workgroup, split into
+//      fp16 hi = rn(xh) and lo = rn(xh - hi) and stored in LDS as MFMA B
+//      fragments: column m < 8 carries hi of row m, column m >= 8 lo of row m - 8.
+//      The activation loads are issued first, so they return first.
+//   2. weight stream: lane l = 16 g + i loads chunk i % 8 (K contiguous words)
+//      of tile (4 r4 + g, 2 c2 + i / 8): one K-word load per lane and group,
+//      DEPTH groups in flight; EARLY of them before the prep barrier, the rest
+//      after it, so that no wave reaches the barrier late because the chip's
+//      memory pipeline refuses its loads.
+//   3. a lane decodes its chunk's 32 weights in registers (the first states
+//      reach into the previous chunk's last word, taken from the neighbouring
+//      lane with DPP) into four MFMA A fragments (rows 0-7 / 8-15 of its tile row
+//      for columns j and j + 8 of its tile, j = i % 8); four 16x16x32 MFMAs per
+//      group accumulate D1 (A row i -> column 32 c2 + i for i < 8, 32 c2 + 8 + i
+//      otherwise) and D2 (32 c2 + 8 + i; 32 c2 + 16 + i).  D[n][m]: lane l holds
+//      m = l % 16, n = 4 (l / 16) + e.
+//   4. epilogue: hi + lo, the P partials of each column pair summed in LDS;
+//      split-K partials are reduced in split order by the last workgroup of
+//      the column group, which applies H128 and sv (src/exl3-ggml.cpp:84-90).
 template <int K>
 struct GemvStream {
-    static constexpr int SLAB = 512 * K;
-    static constexpr int WORDS = 4 * RunGeo<K>::NLOAD;                   // registers per slab and lane
-    static constexpr int DEPTH = WORDS <= 12 ? 4 : (WORDS <= 16 ? 3 : 2);
+    static constexpr int DEPTH = K <= 2 ? 12 : (K <= 4 ? 8 : 4);  // groups in flight per wave
+    static constexpr int EARLY = DEPTH < 3 ? DEPTH : 3;           // of them issued before the prep barrier
 };
-constexpr int kFusedPrepRows = 2;    // rows <= this: activation prep inside the GEMV kernel
-constexpr int kMaxPrepBlocks = 4;    // (kb, row) blocks a wave prepares in the fused path
+constexpr int kGemvPrepMax = 16;          // (kb, row) prep blocks per wave
+constexpr size_t kGemvDummyBytes = 8192;  // >= largest lane offset of a group + its K words (1024 K)
+constexpr size_t kGemvFragLds = 49152;    // LDS budget of the B fragments of a workgroup
 
-// Four agent-coherent loads issued together, then one wait (relaxed atomic loads
-// are otherwise issued one round trip at a time).
-__device__ __forceinline__ float4 load4_coherent(const float *p0, const float *p1, const float *p2, const float *p3) {
-    float4 r;
-    asm volatile(
-        "global_load_dword %0, %4, off sc1\n\t"
-        "global_load_dword %1, %5, off sc1\n\t"
-        "global_load_dword %2, %6, off sc1\n\t"
-        "global_load_dword %3, %7, off sc1\n\t"
-        "s_waitcnt vmcnt(0)"
-        : "=&v"(r.x), "=&v"(r.y), "=&v"(r.z), "=&v"(r.w)
-        : "v"(p0), "v"(p1), "v"(p2), "v"(p3)
-        : "memory");
-    return r;
+// K contiguous words of a chunk, in as few loads as its alignment allows
+template <int K>
+__device__ __forceinline__ void load_chunk(const uint8_t *p, uint32_t (&w)[K]) {
+    if constexpr (K % 4 == 0) {
+#pragma unroll
+        for (int v = 0; v < K / 4; ++v) {
+            const u4 t = __builtin_nontemporal_load((const u4 *)p + v);
+            w[4 * v] = t.x;
+            w[4 * v + 1] = t.y;
+            w[4 * v + 2] = t.z;
+            w[4 * v + 3] = t.w;
+        }
+    } else if constexpr (K % 2 == 0) {
+#pragma unroll
+        for (int v = 0; v < K / 2; ++v) {
+            const u2 t = __builtin_nontemporal_load((const u2 *)p + v);
+            w[2 * v] = t.x;
+            w[2 * v + 1] = t.y;
+        }
+    } else {
+#pragma unroll
+        for (int v = 0; v < K; ++v) w[v] = __builtin_nontemporal_load((const uint32_t *)p + v);
+    }
 }
 
-// Compact B-fragment layout of a slab (128 * rows bytes): 16-byte groups
-// ((hl * rows + r) * 4 + g), hl = 0 hi / 1 lo, r = row, g = lane / 16; element j of
-// a group is k row 16 (g / 2) + R_{g % 2}(j) of the slab.  Lane l of the MFMA
-// B operand reads group (hl, r, g) with m = l % 16 -> (hl, r) = (m / 8, m % 8), or
-// a zero group when r >= rows.
-__device__ __forceinline__ int frag_elem_offset(int rho32, int hl, int r, int rows) {
-    const int kt = rho32 >> 4, r16 = rho32 & 15;
-    const int hh = (r16 >> 2) & 1;
-    const int j = (r16 & 1) | (((r16 >> 3) & 1) << 1) | (((r16 >> 1) & 1) << 2);
-    const int g = 2 * kt + hh;
-    return (((hl * rows + r) * 4 + g) * 8 + j) * 2;  // bytes
-}
-
-// Write hi/lo halves of one prepared activation (row r, k row rho32 of slab ul)
-__device__ __forceinline__ void frag_put(uint8_t *frag, int slab_bytes, int ul, int rho32, int r, int rows, float xv) {
-    const _Float16 h16 = (_Float16)xv;
-    uint8_t *base = frag + (size_t)ul * slab_bytes;
-    *(uint16_t *)(base + frag_elem_offset(rho32, 0, r, rows)) = bitcast<uint16_t>(h16);
-    *(uint16_t *)(base + frag_elem_offset(rho32, 1, r, rows)) = bitcast<uint16_t>((_Float16)(xv - (float)h16));
-}
-
-// hi half at p, lo half at p + lo_off (fragment byte offsets from frag_elem_offset)
-__device__ __forceinline__ void frag_put2(uint8_t *p, int lo_off, float xv) {
-    const _Float16 h16 = (_Float16)xv;
-    *(uint16_t *)p = bitcast<uint16_t>(h16);
-    *(uint16_t *)(p + lo_off) = bitcast<uint16_t>((_Float16)(xv - (float)h16));
-}
-
-// Activation prep kernel for rows > kFusedPrepRows: one workgroup (64 threads =
-// one wave) per (128-row block kb, row r); writes the compact fragments of the
-// four slabs of block kb.  xh = H128(x[r] * su), su from record (0, kb)
-// (src/exl3-ggml.cpp:60-73).
-__global__ __launch_bounds__(64) void gemv_frag_kernel(const uint8_t *__restrict__ records, int bits,
-                                                       const void *__restrict__ x, int x_f16, size_t x_stride,
-                                                       int rows, uint8_t *__restrict__ frag) {
-    const int kb = blockIdx.x, r = blockIdx.y, lane = threadIdx.x;
-    const uint16_t *su = (const uint16_t *)(records + (size_t)kb * group_bytes(bits) + 2048 * bits);
-    float v0 = load_x(x, x_f16, x_stride, r, (size_t)kb * 128 + lane) * half_bits_to_float(su[lane]);
-    float v1 = load_x(x, x_f16, x_stride, r, (size_t)kb * 128 + lane + 64) * half_bits_to_float(su[lane + 64]);
-    h128_wave(v0, v1, lane);
-    const int slab_bytes = 128 * rows;
-    frag_put(frag, slab_bytes, kb * 4 + (lane >> 5), lane & 31, r, rows, v0);
-    frag_put(frag, slab_bytes, kb * 4 + 2 + (lane >> 5), lane & 31, r, rows, v1);
-}
-
-// GEMV.  Workgroup (nb, split s) owns slabs [u0, u1) of the 128-column group nb;
-// wave w takes slabs u0 + w, u0 + w + 4, ... and streams them through its LDS
-// ring (DEPTH slabs in flight).  Per slab a lane decodes, for each tile-column
-// pair tp, one run of tile (k-tile 2 (u % 4) + g / 2, n-tile 2 tp + nl / 8) with
-// c = nl % 8, h = g % 2 (nl = lane % 16, g = lane / 16) and issues two MFMAs
-// (A = decoded W^T fragment, B = activation fragment).  D^T[n][m]: lane l holds
-// m = l % 16, n_local = 4 (l / 16) + e.  Split-K partials are reduced in fixed
-// order by the last workgroup of the column group, which applies H128 and sv
-// (src/exl3-ggml.cpp:84-90).
-template <int K, int CB, bool FUSED>
+template <int K, int CB>
 __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
-    const uint8_t *__restrict__ records, int kbs, int nbs, int splits, int units, const void *__restrict__ x,
-    int x_f16, size_t x_stride, int rows, const uint8_t *__restrict__ frag_global, const uint8_t *__restrict__ dummy,
-    float *__restrict__ partials, unsigned *__restrict__ counters, void *__restrict__ y, int y_f16, size_t y_stride) {
-    using ST = GemvStream<K>;
-    constexpr int NT = kGemvWaves * 64;
+    const uint8_t *__restrict__ records, int kbs, int nbs, int splits, const void *__restrict__ x, int x_f16,
+    size_t x_stride, int rows, const uint8_t *__restrict__ dummy, float *__restrict__ partials,
+    unsigned *__restrict__ counters, void *__restrict__ y, int y_f16, size_t y_stride) {
+    constexpr int W = kGemvWaves;
+    constexpr int P = W / 4;  // waves per column pair
+    constexpr int NT = W * 64;
     constexpr size_t GB = (size_t)2048 * K + 512;
-    constexpr int NW = RunGeo<K>::NW;
-    constexpr int NL = RunGeo<K>::NLOAD;
-    constexpr int D = ST::DEPTH;
+    constexpr int D = GemvStream<K>::DEPTH;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ int last_flag;
-    uint8_t *zero16 = smem;            // 16 zero bytes: B fragment of absent rows
-    uint8_t *frag = smem + 16;
-    const int slab_bytes = 128 * rows;
+    uint8_t *frag = smem;
+    const int blk_bytes = 128 * rows;  // B fragments of one (kb, r4, half): [kg][hl][row] x 16 bytes
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int cp = wave & 3, part = wave >> 2;
     const int s = blockIdx.x / nbs, nb = blockIdx.x - s * nbs;
-    const int u0 = (int)((long long)units * s / splits), u1 = (int)((long long)units * (s + 1) / splits);
-    const int nl = lane & 15, g = lane >> 4;
-    const int c = nl & 7, h = g & 1, ktp = g >> 1;
+    const int kb0 = (int)((long long)kbs * s / splits), kb1 = (int)((long long)kbs * (s + 1) / splits);
+    const int nkb = kb1 - kb0;
     const uint8_t *colgroup = records + (size_t)nb * kbs * GB;
 
-    // 1. activation inputs (issued first: their waits never cover the weight stream)
-    const int kb_first = u0 >> 2, kb_last = (u1 - 1) >> 2;
-    const int nkb = kb_last - kb_first + 1;
+    // 1. activations: all loads first, then the conversions (which wait for them)
     const int nblk = nkb * rows;
-    // raw bits only: converting here would make the compiler wait for these loads
-    // before the weight stream is issued
-    uint32_t px0[FUSED ? kMaxPrepBlocks : 1], px1[FUSED ? kMaxPrepBlocks : 1];
-    uint16_t ps0[FUSED ? kMaxPrepBlocks : 1], ps1[FUSED ? kMaxPrepBlocks : 1];
-    if constexpr (FUSED) {
-        // branch-free so that every load is in flight at once: blocks past nblk
-        // re-read block 0 and are discarded (fused path: rows is 1 or 2)
-        auto prep_loads = [&](auto is_f16) {
-            constexpr bool XF16 = decltype(is_f16)::value;
+    float pv0[kGemvPrepMax], pv1[kGemvPrepMax];
+    auto prep_inputs = [&](auto is_f16) {
+        constexpr bool XF16 = decltype(is_f16)::value;
+        uint32_t px0[kGemvPrepMax], px1[kGemvPrepMax], ps[kGemvPrepMax];
 #pragma unroll
-            for (int q = 0; q < kMaxPrepBlocks; ++q) {
-                const int blk = wave + q * kGemvWaves;
-                const int bc = blk < nblk ? blk : 0;
-                const int kb = kb_first + (rows == 1 ? bc : bc >> 1), r = rows == 1 ? 0 : (bc & 1);
-                const uint16_t *su = (const uint16_t *)(records + (size_t)kb * GB + 2048 * K);  // record (0, kb)
-                const size_t xi = (size_t)r * x_stride + (size_t)kb * 128 + lane;
+        for (int q = 0; q < kGemvPrepMax; ++q) {
+            const int blk = wave + q * W;
+            if (blk < nblk) {
+                const int kbl = blk / rows, r = blk - kbl * rows;
+                const int kb = kb0 + kbl;
+                ps[q] = ((const uint32_t *)(records + (size_t)kb * GB + 2048 * K))[lane];  // record (0, kb): su pair
+                const size_t xi = (size_t)r * x_stride + (size_t)kb * 128 + 2 * lane;
                 if constexpr (XF16) {
                     px0[q] = ((const uint16_t *)x)[xi];
-                    px1[q] = ((const uint16_t *)x)[xi + 64];
+                    px1[q] = ((const uint16_t *)x)[xi + 1];
                 } else {
                     px0[q] = ((const uint32_t *)x)[xi];
-                    px1[q] = ((const uint32_t *)x)[xi + 64];
+                    px1[q] = ((const uint32_t *)x)[xi + 1];
                 }
-                ps0[q] = su[lane];
-                ps1[q] = su[lane + 64];
             }
-        };
-        if (x_f16) prep_loads(std::true_type{});
-        else prep_loads(std::false_type{});
-    }
+        }
+#pragma unroll
+        for (int q = 0; q < kGemvPrepMax; ++q) {
+            if (wave + q * W < nblk) {
+                const float x0 = XF16 ? half_bits_to_float((uint16_t)px0[q]) : bitcast<float>(px0[q]);
+                const float x1 = XF16 ? half_bits_to_float((uint16_t)px1[q]) : bitcast<float>(px1[q]);
+                pv0[q] = x0 * half_bits_to_float((uint16_t)(ps[q] & 0xffffu));
+                pv1[q] = x1 * half_bits_to_float((uint16_t)(ps[q] >> 16));
+            }
+        }
+    };
+    if (x_f16) prep_inputs(std::true_type{});
+    else prep_inputs(std::false_type{});
     // output scales for the epilogue (record (nb, 0), src/exl3-ggml.cpp:84-85)
     const uint16_t *svp = (const uint16_t *)(colgroup + 2048 * K + 256);
     const float sv0 = half_bits_to_float(svp[lane]), sv1 = half_bits_to_float(svp[lane + 64]);
 
-    // 2. weight stream: this wave's slabs u0 + wave + 4 i, i < nw; DEPTH slabs in flight
-    uint32_t off[NL];
-    run_word_offsets<K>(c, h, off);
-#pragma unroll
-    for (int j = 0; j < NL; ++j) off[j] += (uint32_t)((8 * ktp + (nl >> 3)) * 32 * K);
-    const int first_u = u0 + wave;
-    const int nw = first_u < u1 ? (u1 - first_u + kGemvWaves - 1) / kGemvWaves : 0;
-    // wave-uniform slab address: record kb = u / 4, k-tile pair 2 (u % 4); slabs past
-    // the end read a zero region of the workspace, so every issue is unconditional
-    // and the compiler's wait counts stay exact
-    auto slab_src = [&](int i) {
-        const int u = first_u + i * kGemvWaves;
-        return i < nw ? colgroup + (size_t)(u >> 2) * GB + (size_t)(u & 3) * ST::SLAB : dummy;
+    // 2. weight stream: this wave's groups are q = part + P i; issues past its
+    // last group read the workspace's dummy region, so every issue is
+    // unconditional and the compiler's wait counts stay exact
+    const int g = lane >> 4, li = lane & 15, j = li & 7;
+    const uint32_t lane_off = (uint32_t)(((8 * g + 2 * cp + (li >> 3)) * 32 + 4 * j) * K);
+    const int ngroups = (2 * nkb - part + P - 1) / P;
+    auto group_q = [&](int i) { return part + P * i; };
+    auto group_src = [&](int i) -> const uint8_t * {
+        const int q = group_q(i);
+        return i < ngroups ? colgroup + (size_t)(kb0 + (q >> 1)) * GB + (size_t)(q & 1) * 1024 * K + lane_off
+                           : dummy + lane_off;
     };
-    uint32_t buf[D][4][NL];
-    auto issue = [&](int i, uint32_t (&dst)[4][NL]) {
-        const uint8_t *src = slab_src(i);
+    uint32_t buf[D][K];
 #pragma unroll
-        for (int tp = 0; tp < 4; ++tp)
-#pragma unroll
-            for (int j = 0; j < NL; ++j)
-                dst[tp][j] = __builtin_nontemporal_load((const uint32_t *)(src + off[j] + 2 * tp * 32 * K));
-    };
-#pragma unroll
-    for (int d = 0; d < D; ++d) issue(d, buf[d]);
+    for (int d = 0; d < GemvStream<K>::EARLY; ++d) load_chunk<K>(group_src(d), buf[d]);
 
-    // 3. activation fragments of slabs [u0, u1) into LDS
-    if (tid < 4) ((uint32_t *)zero16)[tid] = 0u;
-    if constexpr (FUSED) {
-        const int lane_frag_off = frag_elem_offset(lane & 31, 0, 0, rows);
+    // 3. prep arithmetic under the stream's first latency: H128 per (kb, row),
+    // hi/lo fp16 pairs into the fragment blocks.  Element 2 lane (+1) of block kb
+    // is tile row lane / 8 (r4 = lane / 32, kg = lane / 8 % 4), rows
+    // 2 (lane % 8) (+1): half (lane / 4) % 2, fragment elements 2 (lane % 4) (+1).
+    {
+        const int r4 = lane >> 5, kg = (lane >> 3) & 3, half = (lane >> 2) & 1, jj = 2 * (lane & 3);
 #pragma unroll
-        for (int q = 0; q < kMaxPrepBlocks; ++q) {
-            const int blk = wave + q * kGemvWaves;
+        for (int q = 0; q < kGemvPrepMax; ++q) {
+            const int blk = wave + q * W;
             if (blk < nblk) {
-                const int kb = kb_first + (rows == 1 ? blk : blk >> 1), r = rows == 1 ? 0 : (blk & 1);
-                const float xa = x_f16 ? half_bits_to_float((uint16_t)px0[q]) : bitcast<float>(px0[q]);
-                const float xb = x_f16 ? half_bits_to_float((uint16_t)px1[q]) : bitcast<float>(px1[q]);
-                float v0 = xa * half_bits_to_float(ps0[q]), v1 = xb * half_bits_to_float(ps1[q]);
-                h128_wave(v0, v1, lane);
-                const int ua = kb * 4 + (lane >> 5), ub = kb * 4 + 2 + (lane >> 5);
-                const int eo = lane_frag_off + r * 64;   // + hl * rows * 64 for the lo half
-                if (ua >= u0 && ua < u1) frag_put2(frag + (size_t)(ua - u0) * slab_bytes + eo, rows * 64, v0);
-                if (ub >= u0 && ub < u1) frag_put2(frag + (size_t)(ub - u0) * slab_bytes + eo, rows * 64, v1);
+                const int kbl = blk / rows, r = blk - kbl * rows;
+                float a = pv0[q], b = pv1[q];
+                h128_pair(a, b, lane);
+                const _Float16 ha = (_Float16)a, hb = (_Float16)b;
+                const h2 hi = {ha, hb}, lo = {(_Float16)(a - (float)ha), (_Float16)(b - (float)hb)};
+                uint8_t *bp = frag + (size_t)((kbl * 2 + r4) * 2 + half) * blk_bytes + jj * 2;
+                *(h2 *)(bp + ((kg * 2 + 0) * rows + r) * 16) = hi;
+                *(h2 *)(bp + ((kg * 2 + 1) * rows + r) * 16) = lo;
             }
         }
-    } else {
-        const uint4 *src = (const uint4 *)(frag_global + (size_t)u0 * slab_bytes);
-        uint4 *dst = (uint4 *)frag;
-        for (int t = tid; t < (u1 - u0) * slab_bytes / 16; t += NT) dst[t] = src[t];
     }
     __syncthreads();
+#pragma unroll
+    for (int d = GemvStream<K>::EARLY; d < D; ++d) load_chunk<K>(group_src(d), buf[d]);
 
-    // 4. decode + MFMA
-    const int mrow = nl & 7, mhl = nl >> 3;
-    const bool bvalid = mrow < rows;
-    const int boff = bvalid ? ((mhl * rows + mrow) * 4 + g) * 16 : 0;
-    const uint8_t *bbase = bvalid ? frag : zero16;
-    const int bstride = bvalid ? slab_bytes : 0;
-    f4 acc[4][2];
-#pragma unroll
-    for (int tp = 0; tp < 4; ++tp) acc[tp][0] = acc[tp][1] = (f4){0.f, 0.f, 0.f, 0.f};
-    // words of slab i -> run windows (registers), then refill buf with slab i + D, then decode
-    auto take = [&](int i, const uint32_t (&src)[4][NL], uint32_t (&w)[4][NW]) {
-#pragma unroll
-        for (int tp = 0; tp < 4; ++tp) {
-            if constexpr (RunGeo<K>::ODD) {
-                const uint32_t sh = h ? 16u : 0u;
-#pragma unroll
-                for (int j = 0; j < NW; ++j) w[tp][j] = __builtin_amdgcn_alignbit(src[tp][j], src[tp][j + 1], sh);
-            } else {
-#pragma unroll
-                for (int j = 0; j < NW; ++j) w[tp][j] = src[tp][j];
-            }
-        }
-        (void)i;
-    };
-    auto mac = [&](int i, const uint32_t (&w)[4][NW]) {
-        const int u = first_u + i * kGemvWaves;
-        const h8 b = *(const h8 *)(bbase + (size_t)(u - u0) * bstride + boff);
-#pragma unroll
-        for (int tp = 0; tp < 4; ++tp) {
-            u4 a1, a2;
-            decode_run<K, CB>(w[tp], a1, a2);
-            acc[tp][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<h8>(a1), b, acc[tp][0], 0, 0, 0);
-            acc[tp][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<h8>(a2), b, acc[tp][1], 0, 0, 0);
-        }
+    // 4. decode + MFMA.  B operand lane l: m = l % 16 -> (hl, row) = (m / 8, m % 8),
+    // k group l / 16; rows >= `rows` read the last row (their columns are discarded)
+    const int m = li, hl = m >> 3, mrow = (m & 7) < rows ? (m & 7) : rows - 1;
+    const int boff = ((g * 2 + hl) * rows + mrow) * 16;
+    const bool first_chunk = j == 0;
+    f4 acc1 = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
+    auto mac = [&](int i, const uint32_t (&w)[K]) {
+        // last word of the previous chunk of the same tile: lane i - 1, or i + 7 for chunk 0
+        const uint32_t p1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)w[K - 1], 0x121, 0xF, 0xF, false);  // row_ror:1
+        const uint32_t p9 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)w[K - 1], 0x129, 0xF, 0xF, false);  // row_ror:9
+        u4 fr[4];
+        decode_chunk<K, CB>(w, first_chunk ? p9 : p1, fr);
+        const uint8_t *bp = frag + (size_t)group_q(i) * 2 * blk_bytes + boff;
+        const h8 blo = *(const h8 *)bp, bhi = *(const h8 *)(bp + blk_bytes);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<h8>(fr[0]), blo, acc1, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<h8>(fr[1]), bhi, acc1, 0, 0, 0);
+        acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<h8>(fr[2]), blo, acc2, 0, 0, 0);
+        acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<h8>(fr[3]), bhi, acc2, 0, 0, 0);
     };
     int i0 = 0;
-    for (; i0 + D <= nw; i0 += D) {  // full groups: no branches between issue and use
+    for (; i0 + D <= ngroups; i0 += D) {  // full rounds: no branches between issue and use
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            uint32_t w[4][NW];
-            take(i0 + d, buf[d], w);
-            issue(i0 + d + D, buf[d]);   // words are in registers; refill the slot
-            mac(i0 + d, w);
+            mac(i0 + d, buf[d]);
+            // refill a slot once its words are decoded: loading into registers
+            // still being read would make the compiler rotate the ring with
+            // copies, and a copy of an in-flight load waits for it
+            load_chunk<K>(group_src(i0 + d + D), buf[d]);
         }
     }
 #pragma unroll
-    for (int d = 0; d < D; ++d) {  // tail: fewer than D slabs, already in flight
-        if (i0 + d < nw) {
-            uint32_t w[4][NW];
-            take(i0 + d, buf[d], w);
-            mac(i0 + d, w);
-        }
-    }
+    for (int d = 0; d < D; ++d)  // tail: fewer than D groups, already in flight
+        if (i0 + d < ngroups) mac(i0 + d, buf[d]);
 
-    // 5. epilogue: hi + lo (MFMA column m < 8 gets column m + 8), then the wave sum in LDS
-    __syncthreads();  // every wave is done with the fragments; LDS now holds the wave partials
-    float *red = (float *)smem;
-#pragma unroll
-    for (int tp = 0; tp < 4; ++tp)
-#pragma unroll
-        for (int mf = 0; mf < 2; ++mf)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float v = acc[tp][mf][e];
-                // row_shl:8 -> lane m of each 16-lane row reads lane m + 8 (the lo half)
-                const float o = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x108, 0xF, 0xF, true));
-                if (nl < rows && nl < 8) {
-                    const int nloc = 4 * g + e;
-                    const int col = 16 * (2 * tp + (nloc >> 3)) + (nloc & 7) + 8 * mf;
-                    red[(wave * kGemvMaxRows + nl) * 128 + col] = v + o;
-                }
-            }
-    __syncthreads();
-    constexpr int PER = kGemvMaxRows * 128 / NT;
-    float part[PER];
+    // 5. epilogue: hi + lo (MFMA column m < 8 gets column m + 8) into this wave's
+    // 32 columns of its share of the workgroup partial
+    __syncthreads();  // every wave is done with the fragments; LDS now holds the partials
+    float *red = (float *)smem;  // [P][rows][128]
     const int nval = rows * 128;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int n = 4 * g + e;
+        const float o1 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc1[e]), 0x108, 0xF, 0xF, true));
+        const float o2 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc2[e]), 0x108, 0xF, 0xF, true));
+        if (m < 8 && m < rows) {
+            float *rp = red + part * nval + m * 128 + 32 * cp;
+            rp[n < 8 ? n : 8 + n] = acc1[e] + o1;
+            rp[n < 8 ? 8 + n : 16 + n] = acc2[e] + o2;
+        }
+    }
+    __syncthreads();
+    constexpr int PER = (kGemvMaxRows * 128 + NT - 1) / NT;
+    float psum[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const int t = tid + i * NT;
-        float sum = 0.f;
+        float v = 0.f;
         if (t < nval) {
-            const int rr = t >> 7, col = t & 127;
 #pragma unroll
-            for (int wv = 0; wv < kGemvWaves; ++wv) sum += red[(wv * kGemvMaxRows + rr) * 128 + col];
+            for (int pp = 0; pp < P; ++pp) v += red[pp * nval + t];
         }
-        part[i] = sum;
+        psum[i] = v;
     }
     if (splits > 1) {
         float *mine = partials + ((size_t)nb * splits + s) * (size_t)nval;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int t = tid + i * NT;
-            if (t < nval) store_coherent(mine + t, part[i]);
+            if (t < nval) store_coherent(mine + t, psum[i]);
         }
         if (!arrive_last(counters + nb, (unsigned)splits, &last_flag)) return;
         const float *all = partials + (size_t)nb * splits * (size_t)nval;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int t = tid + i * NT;
-            float sum = 0.f;
-            if (t < nval) {
-                const float *q = all + t;
-                int sp = 0;
-                for (; sp + 4 <= splits; sp += 4) {
-                    const float4 f = load4_coherent(q + (size_t)sp * nval, q + (size_t)(sp + 1) * nval,
-                                                    q + (size_t)(sp + 2) * nval, q + (size_t)(sp + 3) * nval);
-                    sum += f.x;
-                    sum += f.y;
-                    sum += f.z;
-                    sum += f.w;
-                }
-                for (; sp < splits; ++sp) sum += load_coherent(q + (size_t)sp * nval);
-            }
-            part[i] = sum;
+            psum[i] = t < nval ? sum_splits(all + t, splits, (size_t)nval) : 0.f;
         }
         if (tid == 0) reset_counter(counters + nb);  // self-reset for the next call
     }
     // 6. output H128 per row (one wave per row, registers) and sv
-    float *ybuf = red + kGemvWaves * kGemvMaxRows * 128;
+    float *ybuf = red + P * nval;
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const int t = tid + i * NT;
-        if (t < nval) ybuf[t] = part[i];
+        if (t < nval) ybuf[t] = psum[i];
     }
     __syncthreads();
-    for (int rr = wave; rr < rows; rr += kGemvWaves) {
+    for (int rr = wave; rr < rows; rr += W) {
         float a0 = ybuf[rr * 128 + lane], a1 = ybuf[rr * 128 + lane + 64];
         h128_wave(a0, a1, lane);
         a0 *= sv0;
@@ -703,33 +637,36 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
     }
 }
 
+// LDS bytes of a GEMV workgroup: its B fragments, reused after the main loop for
+// the P partials and the output rows
+static size_t gemv_lds_bytes(int nkb_max, size_t rows) {
+    const size_t frag = (size_t)nkb_max * 512 * rows;
+    const size_t red = (size_t)(kGemvWaves / 4 + 1) * rows * 128 * 4;
+    return ((frag > red ? frag : red) + 15) & ~(size_t)15;
+}
+
 GemvPlan gemv_plan(size_t k, size_t n, size_t rows) {
     GemvPlan p{};
     p.nbs = (int)(n / 128);
     p.kbs = (int)(k / 128);
-    p.units = (int)(k / 32);
-    const bool fused = rows <= (size_t)kFusedPrepRows;
     int s = (512 + p.nbs - 1) / (p.nbs > 0 ? p.nbs : 1);
-    const int smax = p.units / 4 > 0 ? p.units / 4 : 1;
-    s = s < 1 ? 1 : (s > smax ? smax : s);
-    // fused prep: a wave prepares at most kMaxPrepBlocks (kb, row) blocks;
-    // fragments of a workgroup must fit next to the ring in LDS
+    s = s < 1 ? 1 : (s > p.kbs ? p.kbs : s);
+    // a workgroup's B fragments must fit its LDS budget and a wave prepares at
+    // most kGemvPrepMax (kb, row) blocks; one kb per workgroup always fits
     for (;;) {
-        const int uwg = (p.units + s - 1) / s;
-        const int nkb = (uwg + 3) / 4 + 1;
-        const bool ok_prep = !fused || nkb * (int)rows <= kMaxPrepBlocks * kGemvWaves;
-        const bool ok_lds = (size_t)uwg * 128 * rows <= 49152;
-        if ((ok_prep && ok_lds) || s >= smax) break;
+        const size_t nkb = ((size_t)p.kbs + s - 1) / s;
+        const bool ok_lds = nkb * 512 * rows <= kGemvFragLds;
+        const bool ok_prep = (nkb * rows + kGemvWaves - 1) / kGemvWaves <= (size_t)kGemvPrepMax;
+        if ((ok_lds && ok_prep) || s >= p.kbs) break;
         ++s;
     }
     p.splits = s;
+    p.nkw = (p.kbs + s - 1) / s;
     size_t off = 0;
     p.counters_off = off;
     off += counter_region_bytes(n);
-    p.dummy_off = off;  // 4 KB target of the stream's issues past the last slab (loaded, never used)
-    off += 4096;
-    p.xprep_off = off;  // compact activation fragments (prep-kernel path)
-    if (!fused) off += ((size_t)p.units * 128 * rows + 255) & ~(size_t)255;
+    p.dummy_off = off;  // target of the stream's issues past a wave's last group (loaded, never used)
+    off += kGemvDummyBytes;
     p.partials_off = off;
     if (s > 1) off += (size_t)p.nbs * s * rows * 128 * 4;
     p.bytes = (off + 255) & ~(size_t)255;
@@ -739,25 +676,11 @@ GemvPlan gemv_plan(size_t k, size_t n, size_t rows) {
 template <int K, int CB>
 static hipError_t launch_gemv_kc(const uint8_t *rec, const void *x, int x_f16, size_t rows, size_t x_stride, void *y,
                                  int y_f16, size_t y_stride, uint8_t *ws, const GemvPlan &p, hipStream_t stream) {
-    const bool fused = rows <= (size_t)kFusedPrepRows;
-    const int uwg = (p.units + p.splits - 1) / p.splits;
-    const size_t frag_bytes = 16 + (size_t)uwg * 128 * rows;
-    const size_t red_bytes = (size_t)kGemvWaves * kGemvMaxRows * 128 * 4 + (size_t)kGemvMaxRows * 128 * 4;
-    size_t lds = frag_bytes > red_bytes ? frag_bytes : red_bytes;
-    lds = (lds + 15) & ~(size_t)15;
+    const size_t lds = gemv_lds_bytes(p.nkw, rows);
     const dim3 grid((unsigned)(p.nbs * p.splits)), block(kGemvWaves * 64);
-    float *part = (float *)(ws + p.partials_off);
-    unsigned *cnt = (unsigned *)(ws + p.counters_off);
-    uint8_t *frag = ws + p.xprep_off;
-    const uint8_t *dummy = ws + p.dummy_off;
-    if (fused) {
-        gemv_kernel<K, CB, true><<<grid, block, lds, stream>>>(rec, p.kbs, p.nbs, p.splits, p.units, x, x_f16, x_stride,
-                                                               (int)rows, nullptr, dummy, part, cnt, y, y_f16, y_stride);
-    } else {
-        gemv_frag_kernel<<<dim3(p.kbs, (unsigned)rows), dim3(64), 0, stream>>>(rec, K, x, x_f16, x_stride, (int)rows, frag);
-        gemv_kernel<K, CB, false><<<grid, block, lds, stream>>>(rec, p.kbs, p.nbs, p.splits, p.units, x, x_f16,
-                                                                x_stride, (int)rows, frag, dummy, part, cnt, y, y_f16, y_stride);
-    }
+    gemv_kernel<K, CB><<<grid, block, lds, stream>>>(rec, p.kbs, p.nbs, p.splits, x, x_f16, x_stride, (int)rows,
+                                                     ws + p.dummy_off, (float *)(ws + p.partials_off),
+                                                     (unsigned *)(ws + p.counters_off), y, y_f16, y_stride);
     return hipGetLastError();
 }
 
@@ -904,9 +827,7 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
         if (!arrive_last(counters + (size_t)mt * nbs + nb, (unsigned)splits, &last_flag)) return;
         const float *all = partials + ((size_t)mt * nbs + nb) * splits * 128 * 128;
         for (int t = tid; t < vrows * 128; t += NT) {
-            float sum = 0.f;
-            for (int sp = 0; sp < splits; ++sp) sum += load_coherent(all + (size_t)sp * 128 * 128 + t);
-            Os[(t >> 7) * OP + (t & 127)] = sum;
+            Os[(t >> 7) * OP + (t & 127)] = sum_splits(all + t, splits, (size_t)128 * 128);
         }
         if (tid == 0) reset_counter(counters + (size_t)mt * nbs + nb);
         __syncthreads();

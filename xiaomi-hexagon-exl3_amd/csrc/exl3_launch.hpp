@@ -10,7 +10,7 @@
 namespace exl3k {
 
 constexpr int kGemvMaxRows = 8;   // GEMV packs hi/lo fp16 halves of up to 8 rows into 16 MFMA columns
-constexpr int kGemvWaves = 4;     // waves per GEMV workgroup
+constexpr int kGemvWaves = 8;     // waves per GEMV workgroup (a multiple of 4)
 constexpr int kGemmBM = 128;      // GEMM rows per workgroup tile
 constexpr int kGemmWaves = 4;
 
@@ -27,8 +27,8 @@ inline size_t counter_region_bytes(size_t n) {
 }
 
 struct GemvPlan {
-    int nbs, kbs, units, splits;  // units = k / 32 slabs
-    size_t counters_off, dummy_off, xprep_off, partials_off, bytes;
+    int nbs, kbs, splits, nkw;  // nkw: largest kb count of a split
+    size_t counters_off, dummy_off, partials_off, bytes;
 };
 struct GemmPlan {
     int nbs, kbs, mtiles, splits;
