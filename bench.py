@@ -44,6 +44,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-gemv", action="store_true", help="headline GEMV only (for profiling)")
+    ap.add_argument("--only-gemm", action="store_true", help="M=512 GEMM only (for profiling)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only time a plain device copy of COPY_BYTES (scales the HBM byte counters)")
     return ap.parse_args()
@@ -140,6 +141,12 @@ def main():
         stop.record(stream)
         torch.cuda.synchronize()
         return start.elapsed_time(stop) / (reps * COPIES), reps * COPIES
+
+    if args.only_gemm:
+        msg, n = timed(512, x512, max(10, args.steps // 10), max(3, args.warmup // 4))
+        print(json.dumps({"gemm_m512_us": round(msg * 1e3, 2), "launches": n,
+                          "tflops": round(2.0 * 512 * K_IN * N_OUT / (msg * 1e-3) / 1e12, 1)}), flush=True)
+        return
 
     # ---- headline: batch 1
     ms1, launches1 = timed(1, xs[1], args.steps, args.warmup)

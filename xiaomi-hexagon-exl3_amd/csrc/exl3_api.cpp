@@ -97,9 +97,15 @@ size_t exl3_hip_mul_mat_workspace_bytes(size_t k, size_t n, size_t rows) {
     size_t need = 0;
     const size_t gemv_rows = rows < (size_t)exl3k::kGemvMaxRows ? rows : (size_t)exl3k::kGemvMaxRows;
     for (size_t r = 1; r <= gemv_rows; ++r) need = std::max(need, exl3k::gemv_plan(k, n, r).bytes);
-    if (rows > (size_t)exl3k::kGemvMaxRows)
-        for (size_t mt = 1; mt <= (rows + exl3k::kGemmBM - 1) / exl3k::kGemmBM; ++mt)
-            need = std::max(need, exl3k::gemm_plan(k, n, std::min(rows, mt * exl3k::kGemmBM)).bytes);
+    // GEMM plans: one tile height per row range, the largest row count of each
+    // m-tile count within it
+    for (size_t r = exl3k::kGemvMaxRows + 1; r <= rows;) {
+        const size_t bm = (size_t)exl3k::gemm_tile_rows(r);
+        const size_t class_end = bm == 128 ? 128 : rows;
+        const size_t r_hi = std::min(rows, std::min(class_end, (r + bm - 1) / bm * bm));
+        need = std::max(need, exl3k::gemm_plan(k, n, r_hi).bytes);
+        r = r_hi + 1;
+    }
     return need;
 }
 

@@ -715,142 +715,318 @@ hipError_t launch_gemv(const void *records, int bits, int cb, size_t k, size_t n
 }
 
 // ============================================================== GEMM
-// Activation prep for the GEMM: xh16[r][i] = fp16(H128(x[r] * su)[i]), rows padded
-// to a multiple of 128 with zeros.  Grid (kbs, mtiles*16), 128 threads, 8 rows each.
-__global__ __launch_bounds__(128) void gemm_xprep_kernel(const uint8_t *__restrict__ records, int bits,
+// Activation prep for the GEMM: xh = fp16(H128(x[r] * su)) (su from record
+// (0, kb), src/exl3-ggml.cpp:60-73), rows padded with zeros to the tile height,
+// stored in MFMA A-fragment order so that the GEMM loads one fragment as one
+// contiguous kilobyte: block (rows 32 rb .. +31, k 128 kb + 16 ks .. +15) is 64
+// lanes x 8 halves, lane l = row % 32 + 32 (k % 16 / 8), element k % 8; blocks
+// ordered (rb, kb, ks).  One wave per (kb, row): elements 2 lane, 2 lane + 1.
+__host__ __device__ inline size_t gemm_xh_offset(int row, int kb, int e, int kbs) {  // halves
+    const int ks = e >> 4, kk = e & 15;
+    const int ln = (row & 31) + 32 * (kk >> 3);
+    return ((((size_t)(row >> 5) * kbs + kb) * 8 + ks) * 64 + ln) * 8 + (kk & 7);
+}
+__global__ __launch_bounds__(256) void gemm_xprep_kernel(const uint8_t *__restrict__ records, int bits,
                                                          const void *__restrict__ x, int x_f16, size_t x_stride,
-                                                         int rows, size_t k, uint16_t *__restrict__ xh16) {
-    __shared__ float v[8 * 129];
-    const int kb = blockIdx.x, t = threadIdx.x, r0 = blockIdx.y * 8;
-    const uint16_t *su = (const uint16_t *)(records + (size_t)kb * group_bytes(bits) + 2048 * bits);
-    const float s = half_bits_to_float(su[t]);
-    for (int r = 0; r < 8; ++r)
-        v[r * 129 + t] = (r0 + r < rows) ? load_x(x, x_f16, x_stride, r0 + r, (size_t)kb * 128 + t) * s : 0.f;
-    __syncthreads();
-    h128_lds(v, 8, 129, t, 128);
-    for (int r = 0; r < 8; ++r) xh16[(size_t)(r0 + r) * k + (size_t)kb * 128 + t] = float_to_half_bits(v[r * 129 + t]);
+                                                         int rows, int rows_padded, int kbs,
+                                                         uint16_t *__restrict__ xh16) {
+    const int lane = threadIdx.x & 63;
+    const int kb = blockIdx.x, r = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (r >= rows_padded) return;
+    const size_t col = (size_t)kb * 128 + 2 * lane;
+    uint32_t out = 0u;
+    if (r < rows) {
+        const uint32_t su2 = ((const uint32_t *)(records + (size_t)kb * group_bytes(bits) + 2048 * bits))[lane];
+        float a = load_x(x, x_f16, x_stride, r, col) * half_bits_to_float((uint16_t)(su2 & 0xffffu));
+        float b = load_x(x, x_f16, x_stride, r, col + 1) * half_bits_to_float((uint16_t)(su2 >> 16));
+        h128_pair(a, b, lane);
+        out = (uint32_t)float_to_half_bits(a) | ((uint32_t)float_to_half_bits(b) << 16);
+    }
+    *(uint32_t *)(xh16 + gemm_xh_offset(r, kb, 2 * lane, kbs)) = out;
 }
 
-// Workgroup (m-tile mt, column group nb, split s): rows [128 mt, +128) x columns
-// [128 nb, +128), records kb in [kb0, kb1).  4 waves in a 2 x 2 grid, each
-// 64 x 64 = 4 x 4 MFMA blocks.  Per record: x tile -> LDS (row-major), record
-// decoded -> LDS n-major (Ws[n][k]), 4 k-steps of 16x16x32 MFMAs.
-template <int K, int CB>
+// GEMM (rows > 8).  Workgroup (split s, m-tile mt, column group nb): rows
+// [BM mt, +BM) x columns [128 nb, +128), records kb in [kb0, kb1); BM = 64 RB
+// rows, wave w owning rows 32 RB w .. +32 RB for all 128 columns: RB x 4
+// accumulator blocks of v_mfma_f32_32x32x16_f16 (one wave per SIMD keeps this
+// MFMA at full rate; the 16x16 one needs two).  Per record kb, software-pipelined
+// in straight-line code per k-step (16 k):
+//   * MFMAs of k-step ks (A = activations, B = decoded weights), the B fragments
+//     of k-step ks + 1 already being read from LDS;
+//   * at odd k-steps, one quarter of the decode of record kb + 1 (fragment
+//     f = ks / 2 of each of the wave's two chunks: the GEMV's chunk decoder) into
+//     the other LDS buffer W[n][k] (fp16, 16-byte k-chunks XOR-swizzled by
+//     n % 16: conflict-free MFMA B reads);
+//   * the activations of k-step ks of record kb + 1 (xh16, fragment-tiled and
+//     L2-resident: every column group reads it), into the registers just consumed.
+// The weight words are loaded two records ahead.  MFMA 32x32x16 operands: A lane l
+// = row l % 32, k 8 (l / 32) + j; B lane l = column l % 32, k 8 (l / 32) + j;
+// D element e of lane l = row (e % 4) + 8 (e / 4) + 4 (l / 32), column l % 32.
+// Split-K partials (kept in the accumulator layout) are summed in split order by
+// the last workgroup of the tile, which applies H128 over the 128 columns of
+// each row in registers (strides 1..16: lanes, 32 and 64: blocks) and sv
+// (src/exl3-ggml.cpp:84-90).
+constexpr int kGemmTargetWgs = 256;  // one 4-wave workgroup per CU (the accumulators fill the register file)
+
+__device__ __forceinline__ int gemm_w_offset(int n, int chunk) {  // halves
+    return n * 128 + ((chunk ^ (n & 15)) << 3);
+}
+
+// Buffer resource over `bytes` bytes at `base`; raw buffer accesses past the
+// end return zeros / are dropped instead of faulting
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+constexpr int kCachePolicySc1 = 16;  // agent-coherent (the encoding of agent-scope atomics)
+
+template <int K, int CB, int RB>
 __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
     const uint8_t *__restrict__ records, int kbs, int nbs, int mtiles, int splits, const uint16_t *__restrict__ xh16,
     size_t k, float *__restrict__ partials, unsigned *__restrict__ counters, void *__restrict__ y, int y_f16,
     size_t y_stride, int rows) {
-    constexpr int NT = kGemmWaves * 64;
-    constexpr int XP = 128 + 8;   // LDS pitch (halves) of the activation and weight tiles
-    constexpr int OP = 128 + 4;   // LDS pitch (floats) of the output tile
+    constexpr int BM = 32 * RB * kGemmWaves;
     constexpr size_t GB = (size_t)2048 * K + 512;
-    constexpr int LDS_BYTES = (2 * 128 * XP * 2) > (128 * OP * 4) ? (2 * 128 * XP * 2) : (128 * OP * 4);
-    __shared__ __attribute__((aligned(16))) uint8_t smem[LDS_BYTES];
+    __shared__ __attribute__((aligned(16))) uint16_t wlds[2][128 * 128];  // 64 KB
     __shared__ int last_flag;
-    uint16_t *Xs = (uint16_t *)smem;
-    uint16_t *Ws = Xs + 128 * XP;
-    float *Os = (float *)smem;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lg = lane >> 4, li = lane & 15, j = li & 7;
+    const int l32 = lane & 31, lh = lane >> 5;
     int bid = blockIdx.x;
-    const int s = bid % splits;
-    bid /= splits;
-    const int nb = bid % nbs, mt = bid / nbs;
+    const int s = bid / (mtiles * nbs);
+    bid -= s * mtiles * nbs;
+    const int mt = bid / nbs, nb = bid - mt * nbs;
+    const int tile = mt * nbs + nb;
     const int kb0 = (int)((long long)kbs * s / splits), kb1 = (int)((long long)kbs * (s + 1) / splits);
+    const uint8_t *colgroup = records + (size_t)nb * kbs * GB;
 
-    f4 acc[4][4];
+    // weights: this wave decodes groups q = 2 wave + h (h = 0, 1) of every record
+    uint32_t wlane[2];
+    int wn0[2], wc0[2];  // column and k-chunk of fragment 0 of each chunk
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int h = 0; h < 2; ++h) {
+        const int q = 2 * wave + h, r4 = q >> 2, c2 = q & 3;
+        wlane[h] = (uint32_t)(r4 * 1024 * K + ((8 * lg + 2 * c2 + (li >> 3)) * 32 + 4 * j) * K);
+        wn0[h] = 16 * (2 * c2 + (li >> 3)) + j;
+        wc0[h] = 2 * (4 * r4 + lg);
+    }
+    auto load_words = [&](int kb, uint32_t (&w)[2][K]) {
+        const uint8_t *rec = colgroup + (size_t)(kb < kb1 ? kb : kb1 - 1) * GB;  // past the end: re-read, unused
+        load_chunk<K>(rec + wlane[0], w[0]);
+        load_chunk<K>(rec + wlane[1], w[1]);
+    };
+    const bool first_chunk = j == 0;
+    // boundary words of the two chunks (see decode_chunk), for the pieces below
+    auto chunk_prepare = [&](const uint32_t (&w)[2][K], uint32_t (&xb)[2][K]) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = (f4){0.f, 0.f, 0.f, 0.f};
-
-    const uint16_t *xbase = xh16 + (size_t)mt * 128 * k;
-    for (int kb = kb0; kb < kb1; ++kb) {
-        // activation tile 128 x 128 fp16: 2048 uint4, 8 per thread
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t p1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)w[h][K - 1], 0x121, 0xF, 0xF, false);
+            const uint32_t p9 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)w[h][K - 1], 0x129, 0xF, 0xF, false);
+            xb[h][0] = __builtin_amdgcn_alignbit(first_chunk ? p9 : p1, w[h][0], 16);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int ch = tid + i * NT;
-            const int row = ch >> 4, c8 = ch & 15;
-            *(uint4 *)(Xs + row * XP + c8 * 8) = *(const uint4 *)(xbase + (size_t)row * k + (size_t)kb * 128 + c8 * 8);
+            for (int m = 1; m < K; ++m) xb[h][m] = __builtin_amdgcn_alignbit(w[h][m - 1], w[h][m], 16);
         }
-        // decode the record: 1024 runs, 4 per thread, into Ws[n][k]
-        const uint8_t *rec = records + ((size_t)nb * kbs + kb) * GB;
+    };
+    // fragment F of both chunks -> LDS: column n0 + 8 (F >> 1), k-chunk c0 + (F & 1)
+    auto decode_piece = [&](auto fc, const uint32_t (&w)[2][K], const uint32_t (&xb)[2][K], uint16_t *dst) {
+        constexpr int F = decltype(fc)::value;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int run = tid + i * NT;
-            const int tile = run >> 4, rc = run & 15;
-            const int c = rc & 7, h = rc >> 3, tr = tile >> 3, tc = tile & 7;
-            uint32_t w[RunGeo<K>::NW];
-            load_run_words<K>((const uint32_t *)(rec + (8 * tr + tc) * 32 * K), c, h, w);
-            u4 a1, a2;
-            decode_run<K, CB>(w, a1, a2);
-            const uint32_t p1[4] = {a1.x, a1.y, a1.z, a1.w}, p2[4] = {a2.x, a2.y, a2.z, a2.w};
+        for (int h = 0; h < 2; ++h) {
+            const u4 fr = chunk_frag<K, CB, F>(w[h], xb[h]);
+            *(u4 *)(dst + gemm_w_offset(wn0[h] + 8 * (F >> 1), wc0[h] + (F & 1))) = fr;
+        }
+    };
+    // activations: A fragment (ks, rb) = the contiguous kilobyte of row block
+    // (BM mt + 32 (RB wave + rb)) / 32, record kb, k-step ks (gemm_xh_offset)
+    const uint16_t *xblk = xh16 + ((size_t)(mt * BM / 32 + RB * wave) * kbs * 8 * 64 + lane) * 8;
+    auto load_x_step = [&](int kb, int ks, h8 (&xs)[RB]) {
+        const uint16_t *p = xblk + ((size_t)(kb < kb1 ? kb : kb1 - 1) * 8 + ks) * 512;
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int kr = tr * 16 + run_slot_row(h, 2 * v);  // even row; pair = rows kr, kr + 1
-                *(uint32_t *)(Ws + (tc * 16 + c) * XP + kr) = p1[v];
-                *(uint32_t *)(Ws + (tc * 16 + c + 8) * XP + kr) = p2[v];
+        for (int rb = 0; rb < RB; ++rb) xs[rb] = *(const h8 *)(p + (size_t)rb * kbs * 8 * 512);
+    };
+    // B fragment (ks, cb): column 32 cb + l32, k-chunk 2 ks + lh; the swizzle term
+    // depends on the lane and k-step only, so the four blocks sit at constant
+    // offsets from one address
+    auto read_b = [&](const uint16_t *wsrc, int ks, h8 (&b)[4]) {
+        const uint16_t *base = wsrc + l32 * 128 + (((2 * ks + lh) ^ li) << 3);
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) b[cb] = *(const h8 *)(base + cb * 32 * 128);
+    };
+
+    f16v acc[RB][4];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[rb][cb][e] = 0.f;
+    auto mma_step = [&](const h8 (&xs)[RB], const h8 (&b)[4]) {
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+                acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xs[rb], b[cb], acc[rb][cb], 0, 0, 0);
+    };
+
+    // prologue: words of kb0 and kb0 + 1, activations of kb0, record kb0 decoded,
+    // B fragments of its first k-step
+    uint32_t wbuf[2][2][K], xb[2][K];
+    h8 xa[8][RB];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) load_x_step(kb0, ks, xa[ks]);
+    load_words(kb0, wbuf[0]);
+    load_words(kb0 + 1, wbuf[1]);
+    chunk_prepare(wbuf[0], xb);
+    decode_piece(std::integral_constant<int, 0>{}, wbuf[0], xb, wlds[0]);
+    decode_piece(std::integral_constant<int, 1>{}, wbuf[0], xb, wlds[0]);
+    decode_piece(std::integral_constant<int, 2>{}, wbuf[0], xb, wlds[0]);
+    decode_piece(std::integral_constant<int, 3>{}, wbuf[0], xb, wlds[0]);
+    __syncthreads();
+    h8 bc[4], bn[4];
+    read_b(wlds[0], 0, bc);
+
+    // one k-step: B of ks + 1 requested, MFMAs of ks, then (odd ks) a decode
+    // piece and the activations of ks for the next record
+    auto kstep = [&](auto kc, int kb, const uint16_t *wcur, uint16_t *wnext, const uint32_t (&wnextw)[2][K],
+                     h8 (&bcur)[4], h8 (&bnxt)[4]) {
+        constexpr int KS = decltype(kc)::value;
+        if constexpr (KS < 7) read_b(wcur, KS + 1, bnxt);
+        mma_step(xa[KS], bcur);
+        if constexpr (KS & 1) decode_piece(std::integral_constant<int, KS / 2>{}, wnextw, xb, wnext);
+        load_x_step(kb + 1, KS, xa[KS]);
+    };
+    // record kb: activations xa, decoded weights wcur (B fragments of k-step 0 in
+    // bc); words of kb + 1 in wnextw; slot wfree takes the words of kb + 2
+    auto step = [&](int kb, const uint16_t *wcur, uint16_t *wnext, uint32_t (&wfree)[2][K],
+                    const uint32_t (&wnextw)[2][K]) {
+        load_words(kb + 2, wfree);
+        chunk_prepare(wnextw, xb);
+        kstep(std::integral_constant<int, 0>{}, kb, wcur, wnext, wnextw, bc, bn);
+        kstep(std::integral_constant<int, 1>{}, kb, wcur, wnext, wnextw, bn, bc);
+        kstep(std::integral_constant<int, 2>{}, kb, wcur, wnext, wnextw, bc, bn);
+        kstep(std::integral_constant<int, 3>{}, kb, wcur, wnext, wnextw, bn, bc);
+        kstep(std::integral_constant<int, 4>{}, kb, wcur, wnext, wnextw, bc, bn);
+        kstep(std::integral_constant<int, 5>{}, kb, wcur, wnext, wnextw, bn, bc);
+        kstep(std::integral_constant<int, 6>{}, kb, wcur, wnext, wnextw, bc, bn);
+        kstep(std::integral_constant<int, 7>{}, kb, wcur, wnext, wnextw, bn, bc);
+        __syncthreads();  // wnext complete; every wave is done reading wcur
+        read_b(wnext, 0, bc);
+    };
+    int kb = kb0;
+    for (; kb + 2 <= kb1; kb += 2) {
+        step(kb, wlds[0], wlds[1], wbuf[0], wbuf[1]);
+        step(kb + 1, wlds[1], wlds[0], wbuf[1], wbuf[0]);
+    }
+    if (kb < kb1) {  // odd count: the last record is in wlds[0]
+#pragma unroll
+        for (int ks = 0; ks < 8; ks += 2) {
+            read_b(wlds[0], ks + 1, bn);
+            mma_step(xa[ks], bc);
+            if (ks + 2 < 8) read_b(wlds[0], ks + 2, bc);
+            mma_step(xa[ks + 1], bn);
+        }
+    }
+
+    // epilogue.  acc[rb][cb][e]: row 32 RB wave + 32 rb + (e % 4) + 8 (e / 4) + 4 lh,
+    // column 32 cb + l32
+    if (splits > 1) {
+        // partials in accumulator layout: [tile][split][wave][rb][cb][v][lane] x 16
+        // bytes (v = e / 4), written and read with agent-coherent buffer accesses
+        constexpr uint32_t kPerSplit = (uint32_t)kGemmWaves * RB * 4 * 4 * 64 * 16;  // bytes
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(partials + (size_t)tile * splits * (kPerSplit / 4),
+                                                    (uint32_t)splits * kPerSplit);
+        const uint32_t lane_off = ((uint32_t)wave * RB * 16 * 64 + lane) * 16;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const u4 d = {__float_as_uint(acc[rb][cb][4 * v]), __float_as_uint(acc[rb][cb][4 * v + 1]),
+                                  __float_as_uint(acc[rb][cb][4 * v + 2]), __float_as_uint(acc[rb][cb][4 * v + 3])};
+                    __builtin_amdgcn_raw_buffer_store_b128(d, rs, (uint32_t)s * kPerSplit + lane_off +
+                                                                      ((rb * 4 + cb) * 4 + v) * 1024, 0, kCachePolicySc1);
+                }
+        if (!arrive_last(counters + tile, (unsigned)splits, &last_flag)) return;
+        // sum all partials (this workgroup's own included) in split order, so the
+        // result does not depend on which workgroup arrived last
+#pragma unroll 1
+        for (int sp = 0; sp < splits; ++sp) {
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const f4 t = bitcast<f4>(__builtin_amdgcn_raw_buffer_load_b128(
+                            rs, (uint32_t)sp * kPerSplit + lane_off + ((rb * 4 + cb) * 4 + v) * 1024, 0,
+                            kCachePolicySc1));
+#pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            acc[rb][cb][4 * v + q] = sp == 0 ? t[q] : acc[rb][cb][4 * v + q] + t[q];
+                    }
+        }
+        if (tid == 0) reset_counter(counters + tile);  // self-reset for the next call
+    }
+    // H128 over the 128 columns of each row, natural stage order: strides 1..16
+    // pair lanes l32 ^ 1..16, strides 32 and 64 pair blocks cb ^ 1, 2
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                float v = acc[rb][cb][e];
+                v = __builtin_fmaf(v, (l32 & 1) ? -1.f : 1.f, lane_xor<1>(v, 0));
+                v = __builtin_fmaf(v, (l32 & 2) ? -1.f : 1.f, lane_xor<2>(v, 0));
+                v = __builtin_fmaf(v, (l32 & 4) ? -1.f : 1.f, lane_xor<4>(v, 0));
+                v = __builtin_fmaf(v, (l32 & 8) ? -1.f : 1.f, lane_xor<8>(v, 0));
+                v = __builtin_fmaf(v, (l32 & 16) ? -1.f : 1.f, lane_xor<16>(v, 0));
+                acc[rb][cb][e] = v;
+            }
+#pragma unroll
+        for (int st = 1; st < 4; st <<= 1)
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+                if (!(cb & st)) {
+                    const f16v a = acc[rb][cb], b = acc[rb][cb | st];
+                    acc[rb][cb] = a + b;
+                    acc[rb][cb | st] = a - b;
+                }
+    }
+    const uint16_t *svp = (const uint16_t *)(colgroup + 2048 * K + 256);  // record (nb, 0)
+    float svv[4];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) svv[cb] = half_bits_to_float(svp[32 * cb + l32]);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int row = mt * BM + 32 * RB * wave + 32 * rb + (e & 3) + 8 * (e >> 2) + 4 * lh;
+            if (row < rows) {
+#pragma unroll
+                for (int cb = 0; cb < 4; ++cb) {
+                    const float v = acc[rb][cb][e] * 0.08838834764831844055f * svv[cb];
+                    const size_t o = (size_t)row * y_stride + (size_t)nb * 128 + 32 * cb + l32;
+                    if (y_f16) ((uint16_t *)y)[o] = float_to_half_bits(v);
+                    else ((float *)y)[o] = v;
+                }
             }
         }
-        __syncthreads();
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            h8 a[4], b[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                a[i] = *(const h8 *)(Xs + (wm * 64 + i * 16 + (lane & 15)) * XP + ks * 32 + 8 * (lane >> 4));
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                b[j] = *(const h8 *)(Ws + (wn * 64 + j * 16 + (lane & 15)) * XP + ks * 32 + 8 * (lane >> 4));
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
-        }
-        __syncthreads();
-    }
-    // D[m][n]: lane l holds n = l % 16, m = 4 (l / 16) + e
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                Os[(wm * 64 + i * 16 + 4 * (lane >> 4) + e) * OP + wn * 64 + j * 16 + (lane & 15)] = acc[i][j][e];
-    __syncthreads();
-    const int row0 = mt * 128;
-    const int vrows = rows - row0 < 128 ? rows - row0 : 128;
-    if (splits > 1) {
-        float *mine = partials + (((size_t)mt * nbs + nb) * splits + s) * 128 * 128;
-        for (int t = tid; t < vrows * 128; t += NT) store_coherent(mine + t, Os[(t >> 7) * OP + (t & 127)]);
-        if (!arrive_last(counters + (size_t)mt * nbs + nb, (unsigned)splits, &last_flag)) return;
-        const float *all = partials + ((size_t)mt * nbs + nb) * splits * 128 * 128;
-        for (int t = tid; t < vrows * 128; t += NT) {
-            Os[(t >> 7) * OP + (t & 127)] = sum_splits(all + t, splits, (size_t)128 * 128);
-        }
-        if (tid == 0) reset_counter(counters + (size_t)mt * nbs + nb);
-        __syncthreads();
-    }
-    h128_lds(Os, vrows, OP, tid, NT);
-    const uint16_t *sv = (const uint16_t *)(records + (size_t)nb * kbs * GB + 2048 * K + 256);
-    for (int t = tid; t < vrows * 128; t += NT) {
-        const int rr = t >> 7, col = t & 127;
-        const float v = Os[rr * OP + col] * half_bits_to_float(sv[col]);
-        const size_t o = (size_t)(row0 + rr) * y_stride + (size_t)nb * 128 + col;
-        if (y_f16) ((uint16_t *)y)[o] = float_to_half_bits(v);
-        else ((float *)y)[o] = v;
-    }
 }
+
+int gemm_tile_rows(size_t rows) { return rows <= 128 ? 128 : 256; }
 
 GemmPlan gemm_plan(size_t k, size_t n, size_t rows) {
     GemmPlan p{};
     p.nbs = (int)(n / 128);
     p.kbs = (int)(k / 128);
-    p.mtiles = (int)((rows + 127) / 128);
+    p.bm = gemm_tile_rows(rows);
+    p.mtiles = (int)((rows + p.bm - 1) / p.bm);
     const int tiles = p.nbs * p.mtiles;
     // split k only below kGemmSplitTiles tiles (then s == 1): counters stay in their region
-    int s = tiles >= (int)kGemmSplitTiles ? 1 : ((int)kGemmSplitTiles + tiles - 1) / tiles;
+    int s = tiles >= (int)kGemmSplitTiles ? 1 : (kGemmTargetWgs + tiles - 1) / tiles;
     const int smax = p.kbs / 4 > 0 ? p.kbs / 4 : 1;
     s = s < 1 ? 1 : (s > smax ? smax : s);
     p.splits = s;
@@ -858,11 +1034,25 @@ GemmPlan gemm_plan(size_t k, size_t n, size_t rows) {
     p.counters_off = off;
     off += counter_region_bytes(n);
     p.xh_off = off;
-    off += (size_t)p.mtiles * 128 * k * 2;
+    off += ((size_t)p.mtiles * p.bm * k * 2 + 255) & ~(size_t)255;
     p.partials_off = off;
-    if (s > 1) off += (size_t)tiles * s * 128 * 128 * 4;
+    if (s > 1) off += (size_t)tiles * s * p.bm * 128 * 4;
     p.bytes = (off + 255) & ~(size_t)255;
     return p;
+}
+
+template <int K, int CB>
+static void launch_gemm_kc(const uint8_t *rec, size_t k, uint16_t *xh, size_t rows, void *y, int y_f16,
+                           size_t y_stride, uint8_t *ws, const GemmPlan &p, hipStream_t stream) {
+    const dim3 grid((unsigned)(p.mtiles * p.nbs * p.splits)), block(kGemmWaves * 64);
+    float *part = (float *)(ws + p.partials_off);
+    unsigned *cnt = (unsigned *)(ws + p.counters_off);
+    if (p.bm == 128)
+        gemm_kernel<K, CB, 1><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, xh, k, part, cnt, y,
+                                                          y_f16, y_stride, (int)rows);
+    else
+        gemm_kernel<K, CB, 2><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, xh, k, part, cnt, y,
+                                                          y_f16, y_stride, (int)rows);
 }
 
 template <int K>
@@ -871,14 +1061,13 @@ static hipError_t launch_gemm_k(const void *records, int cb, size_t k, const voi
                                 hipStream_t stream) {
     const uint8_t *rec = (const uint8_t *)records;
     uint16_t *xh = (uint16_t *)(ws + p.xh_off);
-    gemm_xprep_kernel<<<dim3(p.kbs, p.mtiles * 16), dim3(128), 0, stream>>>(rec, K, x, x_f16, x_stride, (int)rows, k, xh);
-    const dim3 grid((unsigned)(p.mtiles * p.nbs * p.splits)), block(kGemmWaves * 64);
-    float *part = (float *)(ws + p.partials_off);
-    unsigned *cnt = (unsigned *)(ws + p.counters_off);
+    const int rows_padded = p.mtiles * p.bm;
+    gemm_xprep_kernel<<<dim3(p.kbs, (rows_padded + 3) / 4), dim3(256), 0, stream>>>(rec, K, x, x_f16, x_stride,
+                                                                                    (int)rows, rows_padded, p.kbs, xh);
     switch (cb) {
-    case 0: gemm_kernel<K, 0><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, xh, k, part, cnt, y, y_f16, y_stride, (int)rows); break;
-    case 1: gemm_kernel<K, 1><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, xh, k, part, cnt, y, y_f16, y_stride, (int)rows); break;
-    default: gemm_kernel<K, 2><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, xh, k, part, cnt, y, y_f16, y_stride, (int)rows); break;
+    case 0: launch_gemm_kc<K, 0>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream); break;
+    case 1: launch_gemm_kc<K, 1>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream); break;
+    default: launch_gemm_kc<K, 2>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream); break;
     }
     return hipGetLastError();
 }

@@ -11,7 +11,6 @@ namespace exl3k {
 
 constexpr int kGemvMaxRows = 8;   // GEMV packs hi/lo fp16 halves of up to 8 rows into 16 MFMA columns
 constexpr int kGemvWaves = 8;     // waves per GEMV workgroup (a multiple of 4)
-constexpr int kGemmBM = 128;      // GEMM rows per workgroup tile
 constexpr int kGemmWaves = 4;
 
 // Every plan puts its split-K arrival counters in the same leading region, so
@@ -31,12 +30,13 @@ struct GemvPlan {
     size_t counters_off, dummy_off, partials_off, bytes;
 };
 struct GemmPlan {
-    int nbs, kbs, mtiles, splits;
+    int nbs, kbs, bm, mtiles, splits;  // bm: rows per workgroup tile (128 or 256)
     size_t counters_off, xh_off, partials_off, bytes;
 };
 
 GemvPlan gemv_plan(size_t k, size_t n, size_t rows);
 GemmPlan gemm_plan(size_t k, size_t n, size_t rows);
+int gemm_tile_rows(size_t rows);
 
 hipError_t launch_gemv(const void *records, int bits, int cb, size_t k, size_t n, const void *x, int x_f16,
                        size_t rows, size_t x_stride, void *y, int y_f16, size_t y_stride, void *workspace,
