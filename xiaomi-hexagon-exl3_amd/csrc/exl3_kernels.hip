@@ -720,29 +720,63 @@ hipError_t launch_gemv(const void *records, int bits, int cb, size_t k, size_t n
 // stored in MFMA A-fragment order so that the GEMM loads one fragment as one
 // contiguous kilobyte: block (rows 32 rb .. +31, k 128 kb + 16 ks .. +15) is 64
 // lanes x 8 halves, lane l = row % 32 + 32 (k % 16 / 8), element k % 8; blocks
-// ordered (rb, kb, ks).  One wave per (kb, row): elements 2 lane, 2 lane + 1.
+// ordered (rb, kb, ks), so (rb, kb) is one contiguous 8 KB run.
 __host__ __device__ inline size_t gemm_xh_offset(int row, int kb, int e, int kbs) {  // halves
     const int ks = e >> 4, kk = e & 15;
     const int ln = (row & 31) + 32 * (kk >> 3);
     return ((((size_t)(row >> 5) * kbs + kb) * 8 + ks) * 64 + ln) * 8 + (kk & 7);
 }
+// Workgroup (kb, rb), 4 waves x 8 rows; lane: elements 2 lane, 2 lane + 1 of a
+// row (element loads: x needs no alignment beyond its dtype's).  The 8 KB run is
+// assembled in LDS and written with 16-byte stores.
+template <bool XF16>
+__device__ __forceinline__ void xprep_load(const void *__restrict__ x, size_t x_stride, int rows, int r0, size_t col,
+                                           float (&a)[8], float (&b)[8]) {
+    // all eight loads issue before the first use; rows past the end read row 0
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const size_t r = r0 + i < rows ? (size_t)(r0 + i) : 0;
+        if constexpr (XF16) {
+            const uint16_t *p = (const uint16_t *)x + r * x_stride + col;
+            a[i] = half_bits_to_float(p[0]);
+            b[i] = half_bits_to_float(p[1]);
+        } else {
+            const float *p = (const float *)x + r * x_stride + col;
+            a[i] = p[0];
+            b[i] = p[1];
+        }
+    }
+}
 __global__ __launch_bounds__(256) void gemm_xprep_kernel(const uint8_t *__restrict__ records, int bits,
                                                          const void *__restrict__ x, int x_f16, size_t x_stride,
-                                                         int rows, int rows_padded, int kbs,
-                                                         uint16_t *__restrict__ xh16) {
-    const int lane = threadIdx.x & 63;
-    const int kb = blockIdx.x, r = blockIdx.y * 4 + (threadIdx.x >> 6);
-    if (r >= rows_padded) return;
+                                                         int rows, int kbs, uint16_t *__restrict__ xh16) {
+    __shared__ __attribute__((aligned(16))) uint16_t blk[32 * 128];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int kb = blockIdx.x, rb = blockIdx.y;
     const size_t col = (size_t)kb * 128 + 2 * lane;
-    uint32_t out = 0u;
-    if (r < rows) {
-        const uint32_t su2 = ((const uint32_t *)(records + (size_t)kb * group_bytes(bits) + 2048 * bits))[lane];
-        float a = load_x(x, x_f16, x_stride, r, col) * half_bits_to_float((uint16_t)(su2 & 0xffffu));
-        float b = load_x(x, x_f16, x_stride, r, col + 1) * half_bits_to_float((uint16_t)(su2 >> 16));
-        h128_pair(a, b, lane);
-        out = (uint32_t)float_to_half_bits(a) | ((uint32_t)float_to_half_bits(b) << 16);
+    const int r0 = 32 * rb + 8 * wave;
+    const uint32_t su2 = ((const uint32_t *)(records + (size_t)kb * group_bytes(bits) + 2048 * bits))[lane];
+    const float su0 = half_bits_to_float((uint16_t)(su2 & 0xffffu)), su1 = half_bits_to_float((uint16_t)(su2 >> 16));
+    float a[8], b[8];
+    if (x_f16) xprep_load<true>(x, x_stride, rows, r0, col, a, b);
+    else xprep_load<false>(x, x_stride, rows, r0, col, a, b);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        if (r0 + i >= rows) a[i] = b[i] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float e0 = a[i] * su0, e1 = b[i] * su1;
+        h128_pair(e0, e1, lane);
+        *(uint32_t *)(blk + gemm_xh_offset(8 * wave + i, 0, 2 * lane, 1)) =
+            (uint32_t)float_to_half_bits(e0) | ((uint32_t)float_to_half_bits(e1) << 16);
     }
-    *(uint32_t *)(xh16 + gemm_xh_offset(r, kb, 2 * lane, kbs)) = out;
+    __syncthreads();
+    uint16_t *dst = xh16 + gemm_xh_offset(32 * rb, kb, 0, kbs);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int o = (threadIdx.x + 256 * h) * 8;
+        *(uint4 *)(dst + o) = *(const uint4 *)(blk + o);
+    }
 }
 
 // GEMM (rows > 8).  Workgroup (split s, m-tile mt, column group nb): rows
@@ -753,10 +787,10 @@ __global__ __launch_bounds__(256) void gemm_xprep_kernel(const uint8_t *__restri
 // in straight-line code per k-step (16 k):
 //   * MFMAs of k-step ks (A = activations, B = decoded weights), the B fragments
 //     of k-step ks + 1 already being read from LDS;
-//   * at odd k-steps, one quarter of the decode of record kb + 1 (fragment
-//     f = ks / 2 of each of the wave's two chunks: the GEMV's chunk decoder) into
-//     the other LDS buffer W[n][k] (fp16, 16-byte k-chunks XOR-swizzled by
-//     n % 16: conflict-free MFMA B reads);
+//   * one eighth of the decode of record kb + 1 (fragment ks / 2 of the wave's
+//     chunk ks % 2: the GEMV's chunk decoder) into the other LDS buffer W[n][k]
+//     (fp16, 16-byte k-chunks XOR-swizzled by n % 16: conflict-free MFMA B
+//     reads), interleaved with the MFMAs;
 //   * the activations of k-step ks of record kb + 1 (xh16, fragment-tiled and
 //     L2-resident: every column group reads it), into the registers just consumed.
 // The weight words are loaded two records ahead.  MFMA 32x32x16 operands: A lane l
@@ -793,10 +827,16 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lg = lane >> 4, li = lane & 15, j = li & 7;
     const int l32 = lane & 31, lh = lane >> 5;
-    int bid = blockIdx.x;
-    const int s = bid / (mtiles * nbs);
-    bid -= s * mtiles * nbs;
-    const int mt = bid / nbs, nb = bid - mt * nbs;
+    // Workgroups are dispatched to the 8 XCDs round-robin (blockIdx % 8) and each
+    // XCD has its own L2: renumber so that XCD x runs the contiguous range
+    // [x G / 8, (x + 1) G / 8) of the order (split, column group, m-tile), m-tile
+    // fastest.  The m-tiles of one column group then share its weight records,
+    // and the column groups of one split share its activation rows, in one L2.
+    const int G = gridDim.x;
+    int L = (G & 7) ? (int)blockIdx.x : (int)(blockIdx.x & 7) * (G >> 3) + (int)(blockIdx.x >> 3);
+    const int s = L / (mtiles * nbs);
+    L -= s * mtiles * nbs;
+    const int nb = L / mtiles, mt = L - nb * mtiles;
     const int tile = mt * nbs + nb;
     const int kb0 = (int)((long long)kbs * s / splits), kb1 = (int)((long long)kbs * (s + 1) / splits);
     const uint8_t *colgroup = records + (size_t)nb * kbs * GB;
@@ -828,14 +868,12 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
             for (int m = 1; m < K; ++m) xb[h][m] = __builtin_amdgcn_alignbit(w[h][m - 1], w[h][m], 16);
         }
     };
-    // fragment F of both chunks -> LDS: column n0 + 8 (F >> 1), k-chunk c0 + (F & 1)
-    auto decode_piece = [&](auto fc, const uint32_t (&w)[2][K], const uint32_t (&xb)[2][K], uint16_t *dst) {
-        constexpr int F = decltype(fc)::value;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const u4 fr = chunk_frag<K, CB, F>(w[h], xb[h]);
-            *(u4 *)(dst + gemm_w_offset(wn0[h] + 8 * (F >> 1), wc0[h] + (F & 1))) = fr;
-        }
+    // piece P: fragment F = P / 2 of chunk h = P % 2 -> LDS at column
+    // n0 + 8 (F >> 1), k-chunk c0 + (F & 1)
+    auto decode_piece = [&](auto pc, const uint32_t (&w)[2][K], const uint32_t (&xb)[2][K], uint16_t *dst) {
+        constexpr int F = decltype(pc)::value >> 1, h = decltype(pc)::value & 1;
+        const u4 fr = chunk_frag<K, CB, F>(w[h], xb[h]);
+        *(u4 *)(dst + gemm_w_offset(wn0[h] + 8 * (F >> 1), wc0[h] + (F & 1))) = fr;
     };
     // activations: A fragment (ks, rb) = the contiguous kilobyte of row block
     // (BM mt + 32 (RB wave + rb)) / 32, record kb, k-step ks (gemm_xh_offset)
@@ -882,19 +920,36 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
     decode_piece(std::integral_constant<int, 1>{}, wbuf[0], xb, wlds[0]);
     decode_piece(std::integral_constant<int, 2>{}, wbuf[0], xb, wlds[0]);
     decode_piece(std::integral_constant<int, 3>{}, wbuf[0], xb, wlds[0]);
+    decode_piece(std::integral_constant<int, 4>{}, wbuf[0], xb, wlds[0]);
+    decode_piece(std::integral_constant<int, 5>{}, wbuf[0], xb, wlds[0]);
+    decode_piece(std::integral_constant<int, 6>{}, wbuf[0], xb, wlds[0]);
+    decode_piece(std::integral_constant<int, 7>{}, wbuf[0], xb, wlds[0]);
     __syncthreads();
     h8 bc[4], bn[4];
     read_b(wlds[0], 0, bc);
 
-    // one k-step: B of ks + 1 requested, MFMAs of ks, then (odd ks) a decode
-    // piece and the activations of ks for the next record
+    // one k-step: B of ks + 1 requested, MFMAs of ks, a decode piece, then the
+    // activations of ks for the next record
     auto kstep = [&](auto kc, int kb, const uint16_t *wcur, uint16_t *wnext, const uint32_t (&wnextw)[2][K],
                      h8 (&bcur)[4], h8 (&bnxt)[4]) {
         constexpr int KS = decltype(kc)::value;
         if constexpr (KS < 7) read_b(wcur, KS + 1, bnxt);
         mma_step(xa[KS], bcur);
-        if constexpr (KS & 1) decode_piece(std::integral_constant<int, KS / 2>{}, wnextw, xb, wnext);
+        decode_piece(std::integral_constant<int, KS>{}, wnextw, xb, wnext);
         load_x_step(kb + 1, KS, xa[KS]);
+        // One MFMA every few VALU instructions: the wave issues in order, so
+        // MFMAs back to back stall it while the decode waits behind them.  The
+        // B reads lead, the activation loads (seven k-steps ahead of their use:
+        // left alone the scheduler sinks them to the end of the record) trail.
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            if (i < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
+            if (i == 7) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
+            if (i >= 6) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
+        }
+        __builtin_amdgcn_sched_barrier(0);
     };
     // record kb: activations xa, decoded weights wcur (B fragments of k-step 0 in
     // bc); words of kb + 1 in wnextw; slot wfree takes the words of kb + 2
@@ -1062,8 +1117,8 @@ static hipError_t launch_gemm_k(const void *records, int cb, size_t k, const voi
     const uint8_t *rec = (const uint8_t *)records;
     uint16_t *xh = (uint16_t *)(ws + p.xh_off);
     const int rows_padded = p.mtiles * p.bm;
-    gemm_xprep_kernel<<<dim3(p.kbs, (rows_padded + 3) / 4), dim3(256), 0, stream>>>(rec, K, x, x_f16, x_stride,
-                                                                                    (int)rows, rows_padded, p.kbs, xh);
+    gemm_xprep_kernel<<<dim3(p.kbs, rows_padded / 32), dim3(256), 0, stream>>>(rec, K, x, x_f16, x_stride, (int)rows,
+                                                                               p.kbs, xh);
     switch (cb) {
     case 0: launch_gemm_kc<K, 0>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream); break;
     case 1: launch_gemm_kc<K, 1>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream); break;
