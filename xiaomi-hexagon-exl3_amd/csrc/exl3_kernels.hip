@@ -806,22 +806,65 @@ __device__ __forceinline__ int gemm_w_offset(int n, int chunk) {  // halves
     return n * 128 + ((chunk ^ (n & 15)) << 3);
 }
 
-// Buffer resource over `bytes` bytes at `base`; raw buffer accesses past the
-// end return zeros / are dropped instead of faulting
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+
+// Output of accumulator values in the 32x32 MFMA D layout: t[cb][i] is column
+// 32 cb + lane % 32 of row row0 + (i % 4) + 8 (i / 4) + 4 (lane / 32).  H128 over
+// the 128 columns of each row in natural stage order (strides 1..16 pair lanes
+// lane ^ 1..16, strides 32 and 64 pair blocks cb ^ 1, 2; src/exl3_codec.cpp:153-165),
+// then 1/sqrt(128) and sv (src/exl3-ggml.cpp:84-90).
+template <int NE>
+__device__ __forceinline__ void gemm_rows_out(float (&t)[4][NE], int lane, int row0, const uint16_t *svp, int rows,
+                                              void *y, int y_f16, size_t y_stride, size_t col0) {
+    const int l32 = lane & 31, lh = lane >> 5;
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+        for (int i = 0; i < NE; ++i) {
+            float v = t[cb][i];
+            v = __builtin_fmaf(v, (l32 & 1) ? -1.f : 1.f, lane_xor<1>(v, 0));
+            v = __builtin_fmaf(v, (l32 & 2) ? -1.f : 1.f, lane_xor<2>(v, 0));
+            v = __builtin_fmaf(v, (l32 & 4) ? -1.f : 1.f, lane_xor<4>(v, 0));
+            v = __builtin_fmaf(v, (l32 & 8) ? -1.f : 1.f, lane_xor<8>(v, 0));
+            v = __builtin_fmaf(v, (l32 & 16) ? -1.f : 1.f, lane_xor<16>(v, 0));
+            t[cb][i] = v;
+        }
+#pragma unroll
+    for (int st = 1; st < 4; st <<= 1)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+            if (!(cb & st))
+#pragma unroll
+                for (int i = 0; i < NE; ++i) {
+                    const float a = t[cb][i], b = t[cb | st][i];
+                    t[cb][i] = a + b;
+                    t[cb | st][i] = a - b;
+                }
+    float svv[4];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) svv[cb] = half_bits_to_float(svp[32 * cb + l32]);
+#pragma unroll
+    for (int i = 0; i < NE; ++i) {
+        const int row = row0 + (i & 3) + 8 * (i >> 2) + 4 * lh;
+        if (row < rows) {
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) {
+                const float v = t[cb][i] * 0.08838834764831844055f * svv[cb];
+                const size_t o = (size_t)row * y_stride + col0 + 32 * cb + l32;
+                if (y_f16) ((uint16_t *)y)[o] = float_to_half_bits(v);
+                else ((float *)y)[o] = v;
+            }
+        }
+    }
 }
-constexpr int kCachePolicySc1 = 16;  // agent-coherent (the encoding of agent-scope atomics)
 
 template <int K, int CB, int RB>
 __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
     const uint8_t *__restrict__ records, int kbs, int nbs, int mtiles, int splits, const uint16_t *__restrict__ xh16,
-    size_t k, float *__restrict__ partials, unsigned *__restrict__ counters, void *__restrict__ y, int y_f16,
+    size_t k, float *__restrict__ partials, void *__restrict__ y, int y_f16,
     size_t y_stride, int rows) {
     constexpr int BM = 32 * RB * kGemmWaves;
     constexpr size_t GB = (size_t)2048 * K + 512;
     __shared__ __attribute__((aligned(16))) uint16_t wlds[2][128 * 128];  // 64 KB
-    __shared__ int last_flag;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -986,89 +1029,64 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
     // epilogue.  acc[rb][cb][e]: row 32 RB wave + 32 rb + (e % 4) + 8 (e / 4) + 4 lh,
     // column 32 cb + l32
     if (splits > 1) {
-        // partials in accumulator layout: [tile][split][wave][rb][cb][v][lane] x 16
-        // bytes (v = e / 4), written and read with agent-coherent buffer accesses
-        constexpr uint32_t kPerSplit = (uint32_t)kGemmWaves * RB * 4 * 4 * 64 * 16;  // bytes
-        const __amdgpu_buffer_rsrc_t rs = make_rsrc(partials + (size_t)tile * splits * (kPerSplit / 4),
-                                                    (uint32_t)splits * kPerSplit);
-        const uint32_t lane_off = ((uint32_t)wave * RB * 16 * 64 + lane) * 16;
+        // partials in accumulator layout [tile][split][wave][rb][cb][v][lane] x 16
+        // bytes (v = e / 4), summed by gemm_reduce_kernel
+        constexpr size_t kPerSplit = (size_t)kGemmWaves * RB * 4 * 4 * 64 * 4;  // floats
+        float *dst = partials + ((size_t)tile * splits + s) * kPerSplit + (size_t)wave * RB * 16 * 256 + lane * 4;
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
             for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const u4 d = {__float_as_uint(acc[rb][cb][4 * v]), __float_as_uint(acc[rb][cb][4 * v + 1]),
-                                  __float_as_uint(acc[rb][cb][4 * v + 2]), __float_as_uint(acc[rb][cb][4 * v + 3])};
-                    __builtin_amdgcn_raw_buffer_store_b128(d, rs, (uint32_t)s * kPerSplit + lane_off +
-                                                                      ((rb * 4 + cb) * 4 + v) * 1024, 0, kCachePolicySc1);
-                }
-        if (!arrive_last(counters + tile, (unsigned)splits, &last_flag)) return;
-        // sum all partials (this workgroup's own included) in split order, so the
-        // result does not depend on which workgroup arrived last
-#pragma unroll 1
-        for (int sp = 0; sp < splits; ++sp) {
-#pragma unroll
-            for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-                for (int cb = 0; cb < 4; ++cb)
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        const f4 t = bitcast<f4>(__builtin_amdgcn_raw_buffer_load_b128(
-                            rs, (uint32_t)sp * kPerSplit + lane_off + ((rb * 4 + cb) * 4 + v) * 1024, 0,
-                            kCachePolicySc1));
-#pragma unroll
-                        for (int q = 0; q < 4; ++q)
-                            acc[rb][cb][4 * v + q] = sp == 0 ? t[q] : acc[rb][cb][4 * v + q] + t[q];
-                    }
-        }
-        if (tid == 0) reset_counter(counters + tile);  // self-reset for the next call
+                for (int v = 0; v < 4; ++v)
+                    __builtin_nontemporal_store(
+                        (f4){acc[rb][cb][4 * v], acc[rb][cb][4 * v + 1], acc[rb][cb][4 * v + 2], acc[rb][cb][4 * v + 3]},
+                        (f4 *)(dst + ((rb * 4 + cb) * 4 + v) * 256));
+        return;
     }
-    // H128 over the 128 columns of each row, natural stage order: strides 1..16
-    // pair lanes l32 ^ 1..16, strides 32 and 64 pair blocks cb ^ 1, 2
+    const uint16_t *svp = (const uint16_t *)(colgroup + 2048 * K + 256);  // record (nb, 0)
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
+        float t[4][16];
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                float v = acc[rb][cb][e];
-                v = __builtin_fmaf(v, (l32 & 1) ? -1.f : 1.f, lane_xor<1>(v, 0));
-                v = __builtin_fmaf(v, (l32 & 2) ? -1.f : 1.f, lane_xor<2>(v, 0));
-                v = __builtin_fmaf(v, (l32 & 4) ? -1.f : 1.f, lane_xor<4>(v, 0));
-                v = __builtin_fmaf(v, (l32 & 8) ? -1.f : 1.f, lane_xor<8>(v, 0));
-                v = __builtin_fmaf(v, (l32 & 16) ? -1.f : 1.f, lane_xor<16>(v, 0));
-                acc[rb][cb][e] = v;
-            }
-#pragma unroll
-        for (int st = 1; st < 4; st <<= 1)
-#pragma unroll
-            for (int cb = 0; cb < 4; ++cb)
-                if (!(cb & st)) {
-                    const f16v a = acc[rb][cb], b = acc[rb][cb | st];
-                    acc[rb][cb] = a + b;
-                    acc[rb][cb | st] = a - b;
-                }
+            for (int e = 0; e < 16; ++e) t[cb][e] = acc[rb][cb][e];
+        gemm_rows_out<16>(t, lane, mt * BM + 32 * RB * wave + 32 * rb, svp, rows, y, y_f16, y_stride, (size_t)nb * 128);
     }
-    const uint16_t *svp = (const uint16_t *)(colgroup + 2048 * K + 256);  // record (nb, 0)
-    float svv[4];
+}
+
+// Split-K reduction (split count > 1): one wave per (tile, row block blk =
+// RB wave + rb, v) of the GEMM's accumulator layout; lane l sums its 4 x 16
+// bytes of every split in split order (so the result does not depend on the
+// order the GEMM's workgroups ran in), then H128, 1/sqrt(128) and sv over its
+// 8 rows.
+template <int RB>
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(const float *__restrict__ partials, int splits, int nbs,
+                                                          const uint8_t *__restrict__ records, int bits, int kbs,
+                                                          void *__restrict__ y, int y_f16, size_t y_stride, int rows,
+                                                          int nwaves) {
+    constexpr int BM = 32 * RB * kGemmWaves;
+    constexpr size_t kPerSplit = (size_t)kGemmWaves * RB * 4 * 4 * 64 * 4;  // floats
+    const int lane = threadIdx.x & 63;
+    const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (gw >= nwaves) return;
+    const int v = gw & 3, blk = (gw >> 2) % (kGemmWaves * RB), tile = (gw >> 2) / (kGemmWaves * RB);
+    const int mt = tile / nbs, nb = tile - mt * nbs;
+    const float *src = partials + (size_t)tile * splits * kPerSplit + (size_t)blk * 16 * 256 + v * 256 + lane * 4;
+    float t[4][4];
+#pragma unroll 1
+    for (int sp = 0; sp < splits; ++sp) {
+        f4 in[4];
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) svv[cb] = half_bits_to_float(svp[32 * cb + l32]);
+        for (int cb = 0; cb < 4; ++cb) in[cb] = *(const f4 *)(src + (size_t)sp * kPerSplit + cb * 4 * 256);
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
+        for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int row = mt * BM + 32 * RB * wave + 32 * rb + (e & 3) + 8 * (e >> 2) + 4 * lh;
-            if (row < rows) {
-#pragma unroll
-                for (int cb = 0; cb < 4; ++cb) {
-                    const float v = acc[rb][cb][e] * 0.08838834764831844055f * svv[cb];
-                    const size_t o = (size_t)row * y_stride + (size_t)nb * 128 + 32 * cb + l32;
-                    if (y_f16) ((uint16_t *)y)[o] = float_to_half_bits(v);
-                    else ((float *)y)[o] = v;
-                }
-            }
-        }
+            for (int q = 0; q < 4; ++q) t[cb][q] = sp == 0 ? in[cb][q] : t[cb][q] + in[cb][q];
+    }
+    const uint16_t *svp = (const uint16_t *)(records + (size_t)nb * kbs * group_bytes(bits) + 2048 * bits + 256);
+    gemm_rows_out<4>(t, lane, mt * BM + 32 * blk + 8 * v, svp, rows, y, y_f16, y_stride, (size_t)nb * 128);
 }
 
 int gemm_tile_rows(size_t rows) { return rows <= 128 ? 128 : 256; }
@@ -1080,7 +1098,8 @@ GemmPlan gemm_plan(size_t k, size_t n, size_t rows) {
     p.bm = gemm_tile_rows(rows);
     p.mtiles = (int)((rows + p.bm - 1) / p.bm);
     const int tiles = p.nbs * p.mtiles;
-    // split k only below kGemmSplitTiles tiles (then s == 1): counters stay in their region
+    // split k only below kGemmSplitTiles tiles; the split partials are summed by
+    // gemm_reduce_kernel
     int s = tiles >= (int)kGemmSplitTiles ? 1 : (kGemmTargetWgs + tiles - 1) / tiles;
     const int smax = p.kbs / 4 > 0 ? p.kbs / 4 : 1;
     s = s < 1 ? 1 : (s > smax ? smax : s);
@@ -1101,13 +1120,21 @@ static void launch_gemm_kc(const uint8_t *rec, size_t k, uint16_t *xh, size_t ro
                            size_t y_stride, uint8_t *ws, const GemmPlan &p, hipStream_t stream) {
     const dim3 grid((unsigned)(p.mtiles * p.nbs * p.splits)), block(kGemmWaves * 64);
     float *part = (float *)(ws + p.partials_off);
-    unsigned *cnt = (unsigned *)(ws + p.counters_off);
-    if (p.bm == 128)
-        gemm_kernel<K, CB, 1><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, xh, k, part, cnt, y,
-                                                          y_f16, y_stride, (int)rows);
-    else
-        gemm_kernel<K, CB, 2><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, xh, k, part, cnt, y,
-                                                          y_f16, y_stride, (int)rows);
+    const int nwaves = p.mtiles * p.nbs * (p.bm / 8);  // reduction: one wave per 8 rows of a tile
+    const dim3 rgrid((unsigned)((nwaves + 3) / 4));
+    if (p.bm == 128) {
+        gemm_kernel<K, CB, 1><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, xh, k, part, y, y_f16,
+                                                          y_stride, (int)rows);
+        if (p.splits > 1)
+            gemm_reduce_kernel<1><<<rgrid, dim3(256), 0, stream>>>(part, p.splits, p.nbs, rec, K, p.kbs, y, y_f16,
+                                                                   y_stride, (int)rows, nwaves);
+    } else {
+        gemm_kernel<K, CB, 2><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, xh, k, part, y, y_f16,
+                                                          y_stride, (int)rows);
+        if (p.splits > 1)
+            gemm_reduce_kernel<2><<<rgrid, dim3(256), 0, stream>>>(part, p.splits, p.nbs, rec, K, p.kbs, y, y_f16,
+                                                                   y_stride, (int)rows, nwaves);
+    }
 }
 
 template <int K>

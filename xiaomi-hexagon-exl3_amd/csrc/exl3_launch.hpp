@@ -13,17 +13,14 @@ constexpr int kGemvMaxRows = 8;   // GEMV packs hi/lo fp16 halves of up to 8 row
 constexpr int kGemvWaves = 8;     // waves per GEMV workgroup (a multiple of 4)
 constexpr int kGemmWaves = 4;
 
-// Every plan puts its split-K arrival counters in the same leading region, so
-// one workspace serves calls of any row count (and any k) in turn: counters
-// return to zero at the end of every call, and no other region of any plan
-// overlaps them.  The GEMV counts one counter per column group; the GEMM splits
-// k only while it has fewer than kGemmSplitTiles output tiles, so it never
-// needs more counters than that.
+// Every plan starts with the GEMV's split-K arrival counters (one per column
+// group) and places nothing else there, so one workspace serves calls of any
+// row count (and any k) in turn: the counters return to zero at the end of
+// every GEMV call and no GEMM call touches them.  The GEMM splits k only while
+// it has fewer than kGemmSplitTiles output tiles; a second kernel sums its split
+// partials.
 constexpr size_t kGemmSplitTiles = 512;
-inline size_t counter_region_bytes(size_t n) {
-    const size_t slots = n / 128 > kGemmSplitTiles ? n / 128 : kGemmSplitTiles;
-    return (slots * 4 + 255) & ~(size_t)255;
-}
+inline size_t counter_region_bytes(size_t n) { return (n / 128 * 4 + 255) & ~(size_t)255; }
 
 struct GemvPlan {
     int nbs, kbs, splits, nkw;  // nkw: largest kb count of a split
