@@ -726,56 +726,93 @@ __host__ __device__ inline size_t gemm_xh_offset(int row, int kb, int e, int kbs
     const int ln = (row & 31) + 32 * (kk >> 3);
     return ((((size_t)(row >> 5) * kbs + kb) * 8 + ks) * 64 + ln) * 8 + (kk & 7);
 }
-// Workgroup (kb, rb), 4 waves x 8 rows; lane: elements 2 lane, 2 lane + 1 of a
-// row (element loads: x needs no alignment beyond its dtype's).  The 8 KB run is
-// assembled in LDS and written with 16-byte stores.
+// Value of lane lane ^ S (S = 1, 2, 4, 8) inside each row of 16 lanes, by DPP
+// (row_ror:n gives lane i the value of lane (i - n) mod 16).
+template <int S>
+__device__ __forceinline__ float dpp_xor(float v) {
+    const int iv = __float_as_int(v);
+    if constexpr (S == 1) {
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xF, 0xF, false));  // quad_perm 1,0,3,2
+    } else if constexpr (S == 2) {
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xF, 0xF, false));  // quad_perm 2,3,0,1
+    } else if constexpr (S == 4) {
+        // lanes 0-3 and 8-11 of the row (banks 0, 2) read lane + 4 (row_ror:12),
+        // lanes 4-7 and 12-15 (banks 1, 3) read lane - 4 (row_ror:4)
+        const int t = __builtin_amdgcn_update_dpp(iv, iv, 0x12C, 0xF, 0x5, false);
+        return __int_as_float(__builtin_amdgcn_update_dpp(t, iv, 0x124, 0xF, 0xA, false));
+    } else {
+        static_assert(S == 8, "dpp_xor: S in 1, 2, 4, 8");
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, iv, 0x128, 0xF, 0xF, false));  // row_ror:8
+    }
+}
+
+// Workgroup (kb, rb), 4 waves x 8 rows (two passes of 4); lane 16 g + i holds
+// elements 8 i .. 8 i + 7 of row 32 rb + 8 wave + 4 pass + g.  H128 stages 1, 2
+// and 4 are inside the lane, 8 .. 64 pair lanes i ^ 1 .. 8 (DPP); the lane's
+// eight results are one 16-byte unit of the fragment layout, stored directly.
 template <bool XF16>
-__device__ __forceinline__ void xprep_load(const void *__restrict__ x, size_t x_stride, int rows, int r0, size_t col,
-                                           float (&a)[8], float (&b)[8]) {
-    // all eight loads issue before the first use; rows past the end read row 0
+__device__ __forceinline__ void xprep_load(const void *__restrict__ x, const size_t (&off)[2], float (&v)[2][8]) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const size_t r = r0 + i < rows ? (size_t)(r0 + i) : 0;
+    for (int ps = 0; ps < 2; ++ps) {
         if constexpr (XF16) {
-            const uint16_t *p = (const uint16_t *)x + r * x_stride + col;
-            a[i] = half_bits_to_float(p[0]);
-            b[i] = half_bits_to_float(p[1]);
+            const uint16_t *p = (const uint16_t *)x + off[ps];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[ps][j] = half_bits_to_float(p[j]);
         } else {
-            const float *p = (const float *)x + r * x_stride + col;
-            a[i] = p[0];
-            b[i] = p[1];
+            const float *p = (const float *)x + off[ps];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[ps][j] = p[j];
         }
     }
 }
 __global__ __launch_bounds__(256) void gemm_xprep_kernel(const uint8_t *__restrict__ records, int bits,
                                                          const void *__restrict__ x, int x_f16, size_t x_stride,
                                                          int rows, int kbs, uint16_t *__restrict__ xh16) {
-    __shared__ __attribute__((aligned(16))) uint16_t blk[32 * 128];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, i = lane & 15;
     const int kb = blockIdx.x, rb = blockIdx.y;
-    const size_t col = (size_t)kb * 128 + 2 * lane;
-    const int r0 = 32 * rb + 8 * wave;
-    const uint32_t su2 = ((const uint32_t *)(records + (size_t)kb * group_bytes(bits) + 2048 * bits))[lane];
-    const float su0 = half_bits_to_float((uint16_t)(su2 & 0xffffu)), su1 = half_bits_to_float((uint16_t)(su2 >> 16));
-    float a[8], b[8];
-    if (x_f16) xprep_load<true>(x, x_stride, rows, r0, col, a, b);
-    else xprep_load<false>(x, x_stride, rows, r0, col, a, b);
+    const size_t col = (size_t)kb * 128 + 8 * i;
+    const uint4 su8 = *(const uint4 *)(records + (size_t)kb * group_bytes(bits) + 2048 * bits + 16 * i);
+    const uint32_t suw[4] = {su8.x, su8.y, su8.z, su8.w};
+    float v[2][8];
+    size_t off[2];  // rows past the end read row 0
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-        if (r0 + i >= rows) a[i] = b[i] = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        float e0 = a[i] * su0, e1 = b[i] * su1;
-        h128_pair(e0, e1, lane);
-        *(uint32_t *)(blk + gemm_xh_offset(8 * wave + i, 0, 2 * lane, 1)) =
-            (uint32_t)float_to_half_bits(e0) | ((uint32_t)float_to_half_bits(e1) << 16);
+    for (int ps = 0; ps < 2; ++ps) {
+        const int r = 32 * rb + 8 * wave + 4 * ps + g;
+        off[ps] = (size_t)(r < rows ? r : 0) * x_stride + col;
     }
-    __syncthreads();
-    uint16_t *dst = xh16 + gemm_xh_offset(32 * rb, kb, 0, kbs);
+    if (x_f16) xprep_load<true>(x, off, v);  // all loads before the first use
+    else xprep_load<false>(x, off, v);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int o = (threadIdx.x + 256 * h) * 8;
-        *(uint4 *)(dst + o) = *(const uint4 *)(blk + o);
+    for (int ps = 0; ps < 2; ++ps) {
+        const int r = 32 * rb + 8 * wave + 4 * ps + g;
+        float *e = v[ps];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            e[j] = r < rows ? e[j] * half_bits_to_float((uint16_t)(suw[j >> 1] >> (16 * (j & 1)))) : 0.f;
+#pragma unroll
+        for (int st = 1; st < 8; st <<= 1)
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (!(j & st)) {
+                    const float a = e[j], b = e[j | st];
+                    e[j] = a + b;
+                    e[j | st] = a - b;
+                }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            float t = e[j];
+            t = __builtin_fmaf(t, (i & 1) ? -1.f : 1.f, dpp_xor<1>(t));
+            t = __builtin_fmaf(t, (i & 2) ? -1.f : 1.f, dpp_xor<2>(t));
+            t = __builtin_fmaf(t, (i & 4) ? -1.f : 1.f, dpp_xor<4>(t));
+            t = __builtin_fmaf(t, (i & 8) ? -1.f : 1.f, dpp_xor<8>(t));
+            e[j] = t * 0.08838834764831844055f;
+        }
+        uint4 out;
+        out.x = (uint32_t)float_to_half_bits(e[0]) | ((uint32_t)float_to_half_bits(e[1]) << 16);
+        out.y = (uint32_t)float_to_half_bits(e[2]) | ((uint32_t)float_to_half_bits(e[3]) << 16);
+        out.z = (uint32_t)float_to_half_bits(e[4]) | ((uint32_t)float_to_half_bits(e[5]) << 16);
+        out.w = (uint32_t)float_to_half_bits(e[6]) | ((uint32_t)float_to_half_bits(e[7]) << 16);
+        *(uint4 *)(xh16 + gemm_xh_offset(r, kb, 8 * i, kbs)) = out;
     }
 }
 
@@ -1076,14 +1113,22 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float *__restric
     const float *src = partials + (size_t)tile * splits * kPerSplit + (size_t)blk * 16 * 256 + v * 256 + lane * 4;
     float t[4][4];
 #pragma unroll 1
-    for (int sp = 0; sp < splits; ++sp) {
-        f4 in[4];
+    for (int sp0 = 0; sp0 < splits; sp0 += 4) {  // loads of four splits in flight, then their sum in order
+        f4 in[4][4];
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) in[cb] = *(const f4 *)(src + (size_t)sp * kPerSplit + cb * 4 * 256);
+        for (int u = 0; u < 4; ++u) {
+            const int sp = sp0 + u < splits ? sp0 + u : splits - 1;
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb)
+            for (int cb = 0; cb < 4; ++cb) in[u][cb] = *(const f4 *)(src + (size_t)sp * kPerSplit + cb * 4 * 256);
+        }
 #pragma unroll
-            for (int q = 0; q < 4; ++q) t[cb][q] = sp == 0 ? in[cb][q] : t[cb][q] + in[cb][q];
+        for (int u = 0; u < 4; ++u)
+            if (sp0 + u < splits)
+#pragma unroll
+                for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        t[cb][q] = sp0 + u == 0 ? in[u][cb][q] : t[cb][q] + in[u][cb][q];
     }
     const uint16_t *svp = (const uint16_t *)(records + (size_t)nb * kbs * group_bytes(bits) + 2048 * bits + 256);
     gemm_rows_out<4>(t, lane, mt * BM + 32 * blk + 8 * v, svp, rows, y, y_f16, y_stride, (size_t)nb * 128);
