@@ -15,6 +15,10 @@
  *   exl3_hip_decode       <- exl3::decode_inner(_slice) src/exl3_codec.cpp:123-145
  *                            (and exl3_iface_decode src/hexagon/exl3_iface.idl:5-7)
  *   exl3_hip_reconstruct  <- exl3::reconstruct(_slice)  src/exl3_codec.cpp:169-204
+ *   exl3_hip_get_rows     <- ggml_exl3_get_rows        src/exl3-ggml.cpp:19-49,
+ *                            declared include/exl3-block.h:47, dispatched from
+ *                            ggml_compute_forward_get_rows (patches/llama-exl3.patch:114-121);
+ *                            tied embedding exl3::Model::embedding src/exl3_model.cpp:168-187
  *   exl3_hip_codebook     <- exl3::decode_codebook      src/exl3_codec.cpp:68-86
  *   exl3_hip_hadamard128  <- exl3::hadamard128          src/exl3_codec.cpp:147-167
  *   exl3_hip_pack_records <- record assembly tests/test-exl3-graph.cpp:110-118,
@@ -109,6 +113,20 @@ exl3_status exl3_hip_reconstruct(const void *src, exl3_layout layout, const uint
                                  const uint16_t *sv, unsigned bits, unsigned codebook, size_t k,
                                  size_t n, size_t first_column, size_t column_count, uint16_t *out,
                                  hipStream_t stream);
+
+/* GET_ROWS: out[r][0..k) = column ids[r] of the original-basis weight
+ * diag(su) H W_hat H diag(sv), i.e. for every kb the reconstruct of record
+ * (ids[r] / 128, kb) as a 128x128 matrix (exl3::reconstruct, fp16-rounded),
+ * column ids[r] % 128; bit-exact, widened to fp32 for ot = F32 (ggml's dst type).
+ *   records        device, as exl3_hip_mul_mat; codebook: the reference uses mul1 = 2
+ *   ids            device int32[count] (GGML_TYPE_I32 ids)
+ *   out            device, count rows of ot, row stride out_row_stride (>= k) elements
+ *   bad_ids        optional device int: set to 1 when some id is outside [0, n)
+ *                  (its row is NaN); the reference asserts instead
+ * count == 0 is a no-op. */
+exl3_status exl3_hip_get_rows(const void *records, unsigned bits, unsigned codebook, size_t k, size_t n,
+                              const int32_t *ids, size_t count, void *out, exl3_dtype ot, size_t out_row_stride,
+                              int *bad_ids, hipStream_t stream);
 
 /* out[i] = fp16 codebook value of states[i], bit-exact with exl3::decode_codebook. */
 exl3_status exl3_hip_codebook(const uint16_t *states, size_t count, unsigned codebook, uint16_t *out,

@@ -22,6 +22,8 @@
  *     (tools/exl3_verify.cpp:57-66).
  *   - orc_pack_records / orc_decode_records: record offsets re-derived from
  *     include/exl3-block.h and checked against decode_inner of the tile grid.
+ *   - orc_get_rows: column ids[r] of orc_reconstruct over the whole matrix, and
+ *     the zero-trellis closed form (tests/test_model_reader.cpp:51-56).
  *   - orc_mul_mat: float64 x . reconstruct(W) with the compiled reference
  *     reconstruct, NMSE < 1e-5 (the gate of tests/test-exl3-graph.cpp:100-104),
  *     and planted-mistake tests showing that gate catches a dropped su/sv, a
@@ -281,6 +283,34 @@ int orc_reconstruct(const uint16_t *packed, const uint16_t *su, const uint16_t *
                     size_t n, unsigned bits, unsigned cb, uint16_t *out)
 {
     return orc_reconstruct_slice(packed, su, sv, k, n, 0, n, bits, cb, out);
+}
+
+/* src/exl3-ggml.cpp:19-49 (ggml_exl3_get_rows): out[r][128 kb + i] =
+ * float(reconstruct of record (ids[r] / 128, kb) as a 128x128 matrix)[i][ids[r] % 128]. */
+int orc_get_rows(const void *records, unsigned bits, unsigned cb, size_t k, size_t n, const int32_t *ids,
+                 size_t count, float *out, size_t out_stride)
+{
+    if (!valid_rate(bits, cb) || !valid_shape(k, n, 128) || out_stride < k) return ORC_EINVAL;
+    for (size_t r = 0; r < count; ++r)
+        if (ids[r] < 0 || (size_t)ids[r] >= n) return ORC_EINVAL;
+    uint16_t *dec = (uint16_t *)malloc(128u * 128u * sizeof(uint16_t));
+    if (!dec) return ORC_EINVAL;
+    const size_t gb = orc_group_bytes(bits);
+    for (size_t r = 0; r < count; ++r) {
+        const size_t id = (size_t)ids[r];
+        for (size_t kb = 0; kb < k / 128; ++kb) {
+            const unsigned char *g = (const unsigned char *)records + ((id / 128) * (k / 128) + kb) * gb;
+            const int rc = orc_reconstruct((const uint16_t *)g, (const uint16_t *)(g + 2048u * bits),
+                                           (const uint16_t *)(g + 2048u * bits + 256u), 128, 128, bits, cb, dec);
+            if (rc) {
+                free(dec);
+                return rc;
+            }
+            for (size_t i = 0; i < 128; ++i) out[r * out_stride + kb * 128 + i] = orc_half_to_float(dec[i * 128 + id % 128]);
+        }
+    }
+    free(dec);
+    return ORC_OK;
 }
 
 /* --------------------------------------------------------- record layout */

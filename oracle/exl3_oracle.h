@@ -55,6 +55,13 @@ int orc_reconstruct(const uint16_t *packed, const uint16_t *su, const uint16_t *
                     size_t n, unsigned bits, unsigned cb, uint16_t *out);
 
 /* ---- 128x128 group-record layout (include/exl3-block.h:5-14,34-39) ---- */
+
+/* GET_ROWS on records (src/exl3-ggml.cpp:19-49): out[r][0..k) (row stride
+ * out_stride floats) = column ids[r] of the original-basis weight, each record's
+ * 128x128 reconstruct rounded to fp16 and widened; ORC_EINVAL on an id outside
+ * [0, n) (the reference asserts). */
+int orc_get_rows(const void *records, unsigned bits, unsigned cb, size_t k, size_t n, const int32_t *ids,
+                 size_t count, float *out, size_t out_stride);
 size_t orc_group_bytes(unsigned bits); /* include/exl3-block.h:14 */
 
 /* upstream tiles + su + sv -> records, tests/test-exl3-graph.cpp:110-118 and

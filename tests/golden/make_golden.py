@@ -11,6 +11,10 @@ Outputs (all data, no code):
     layer.npz       a small EXL3 layer: records, x, y (float64 expectation)
     *.exl3ref       two fixtures in the reference's EXL3REF1 format
                     (tools/exl3_verify.cpp:10, tests/generate_cuda_fixtures.py:82-85)
+    get_rows.npz    GET_ROWS expectations computed the way ggml_exl3_get_rows
+                    does (src/exl3-ggml.cpp:29-43): the reference exl3::reconstruct
+                    of each 128x128 record, column id % 128, widened to fp32
+Sections can be named to regenerate only those: make_golden.py get_rows
 """
 import hashlib
 import json
@@ -48,8 +52,34 @@ def h128_matrix():
     return h / np.sqrt(128.0)
 
 
+def get_rows_fixture(ref):
+    k, n, bits, cb, seed = 256, 384, 6, 2, 7007
+    p = synth.packed_tiles(seed, k, n, bits)
+    su, sv = synth.layer_scales(seed, k, n)
+    records = synth.pack_records(p, su, sv, bits).view(np.uint8)
+    gb = synth.group_bytes(bits)
+    ids = np.array([0, n // 2, n - 1, 128, 5, 255, n - 1], dtype=np.int32)
+    out = np.zeros((ids.size, k), dtype=np.float32)
+    for r, i in enumerate(ids):
+        for kb in range(k // 128):
+            g = records[(i // 128 * (k // 128) + kb) * gb:][:gb]
+            tiles = g[: 2048 * bits].view(np.uint16)
+            gsu = g[2048 * bits: 2048 * bits + 256].view(np.float16)
+            gsv = g[2048 * bits + 256: 2048 * bits + 512].view(np.float16)
+            blk = ref.reconstruct(tiles, gsu, gsv, 128, 128, bits, cb)
+            out[r, kb * 128:(kb + 1) * 128] = blk[:, i % 128].view(np.float16).astype(np.float32)
+    np.savez(HERE / "get_rows.npz", meta=np.array([k, n, bits, cb, seed]), ids=ids, out=out,
+             records_sha256=np.array(sha(records)))
+
+
 def main():
     ref = Reference()
+    only = sys.argv[1:]
+    if only:
+        for name in only:
+            {"get_rows": get_rows_fixture}[name](ref)
+        print("golden fixtures written to", HERE)
+        return
     # 1. codebooks
     cbj = {}
     spots = list(range(0, 65536, 257)) + [65535]
@@ -125,6 +155,8 @@ def main():
             f.write(b"EXL3REF1" + struct.pack("<4I", k, n, bits, cb))
             for a in (p.astype("<u2"), su.view("<u2"), sv.view("<u2"), inner.astype("<u2"), orig.astype("<u2")):
                 f.write(np.ascontiguousarray(a).tobytes())
+    # 7. GET_ROWS
+    get_rows_fixture(ref)
     print("golden fixtures written to", HERE)
 
 

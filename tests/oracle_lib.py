@@ -46,10 +46,21 @@ class Oracle:
                                   ctypes.c_int, _sz, _sz, _f32p, _sz, ctypes.c_uint]
         L.orc_mul_mat_groups.argtypes = [ctypes.c_void_p, ctypes.c_uint, ctypes.c_uint, _sz, _sz, ctypes.c_void_p,
                                          ctypes.c_int, _sz, _sz, _f32p, _sz, ctypes.c_uint, _sz, _sz]
+        L.orc_get_rows.argtypes = [ctypes.c_void_p, ctypes.c_uint, ctypes.c_uint, _sz, _sz, ctypes.c_void_p, _sz,
+                                   _f32p, _sz]
         self.L = L
 
     def codebook_table(self, cb):
         return np.array([self.L.orc_decode_codebook(s, cb) for s in range(65536)], dtype=np.uint16)
+
+    def get_rows(self, records, bits, cb, k, n, ids):
+        """ggml_exl3_get_rows: [len(ids), k] float32"""
+        r = np.ascontiguousarray(records)
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        out = np.zeros((ids.size, k), dtype=np.float32)
+        if self.L.orc_get_rows(_ptr(r), bits, cb, k, n, _ptr(ids), ids.size, _ptr(out, _f32p), k):
+            raise ValueError("get_rows rejected its arguments")
+        return out
 
     def decode_tile(self, packed, bits, cb):
         p = np.ascontiguousarray(packed, dtype=np.uint16)

@@ -58,6 +58,9 @@ def test_host_side_status_and_planning():
     # rejected arguments never reach the device
     assert L.exl3_hip_mul_mat(None, 4, 2, 128, 128, None, 1, 1, 128, None, 0, 128, None, 0, None) == 1
     assert L.exl3_hip_decode(None, 0, 4, 2, 16, 16, 0, 16, None, None) == 1
+    assert L.exl3_hip_get_rows(None, 4, 2, 128, 128, None, 1, None, 0, 128, None, None) == 1
+    assert L.exl3_hip_get_rows(None, 4, 2, 100, 128, None, 1, None, 0, 128, None, None) == 1
+    assert L.exl3_hip_get_rows(None, 4, 2, 128, 128, None, 0, None, 0, 128, None, None) == 0  # count 0: no-op
     assert L.exl3_hip_hadamard128(None, 100, None) == 1
     assert L.exl3_hip_status_string(3) == b"workspace too small"
 

@@ -178,6 +178,49 @@ def test_model_reader_known_answer(oracle):
     assert np.all(w.view(np.float16).reshape(-1)[1:] == 0)
 
 
+# ---- GET_ROWS (src/exl3-ggml.cpp:19-49) ---------------------------------------------
+
+def test_get_rows_golden(oracle):
+    d = np.load(GOLD / "get_rows.npz")
+    k, n, bits, cb, seed = (int(v) for v in d["meta"])
+    p = synth.packed_tiles(seed, k, n, bits)
+    su, sv = synth.layer_scales(seed, k, n)
+    rec = synth.pack_records(p, su, sv, bits).view(np.uint8)
+    assert sha(rec) == str(d["records_sha256"])
+    got = oracle.get_rows(rec, bits, cb, k, n, d["ids"])
+    assert np.array_equal(got.view(np.uint32), d["out"].view(np.uint32))
+
+
+@pytest.mark.parametrize("bits,cb", [(4, 2), (3, 0), (6, 1)])
+def test_get_rows_is_a_reconstruct_column(oracle, bits, cb):
+    # each id's row is column id of the whole-matrix reconstruct (su from the record's
+    # kb, sv from its nb): catches a wrong record, column or transposition
+    k, n = 256, 384
+    p = synth.packed_tiles(31 + bits, k, n, bits)
+    su, sv = synth.layer_scales(31 + bits, k, n)
+    rec = synth.pack_records(p, su, sv, bits).view(np.uint8)
+    ids = np.array([0, n // 2, n - 1, 127, 128, 300], dtype=np.int32)
+    full = oracle.reconstruct(p, su, sv, k, n, bits, cb).view(np.float16).astype(np.float32)
+    got = oracle.get_rows(rec, bits, cb, k, n, ids)
+    assert np.array_equal(got, full[:, ids].T)
+
+
+def test_get_rows_model_reader_known_answer(oracle):
+    # tests/test_model_reader.cpp:51-56 through GET_ROWS: zero trellis, su = sv = 1:
+    # row 0 = [fp16(128 code(0)), 0, ...], row 1 = zeros (H 1 = sqrt(128) e0)
+    k = n = 128
+    p = np.zeros((k // 16, n // 16, 16 * 4), np.uint16)
+    one = np.ones(128, np.float16)
+    rec = synth.pack_records(p, one, one, 4).view(np.uint8)
+    got = oracle.get_rows(rec, 4, 2, k, n, np.array([0, 1], np.int32))
+    code = oracle.L.orc_half_to_float(oracle.L.orc_decode_codebook(0, 2))
+    assert got[0, 0] == np.float16(code * 128) and np.all(got[0, 1:] == 0) and np.all(got[1] == 0)
+    with pytest.raises(ValueError):
+        oracle.get_rows(rec, 4, 2, k, n, np.array([0, n], np.int32))
+    with pytest.raises(ValueError):
+        oracle.get_rows(rec, 4, 2, k, n, np.array([-1], np.int32))
+
+
 # ---- records --------------------------------------------------------------------
 
 def test_pack_records_matches_numpy_and_decodes(oracle):

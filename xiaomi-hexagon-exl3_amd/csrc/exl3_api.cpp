@@ -166,6 +166,18 @@ exl3_status exl3_hip_reconstruct(const void *src, exl3_layout layout, const uint
                                               n, first_column, column_count, out, stream));
 }
 
+exl3_status exl3_hip_get_rows(const void *records, unsigned bits, unsigned codebook, size_t k, size_t n,
+                              const int32_t *ids, size_t count, void *out, exl3_dtype ot, size_t out_row_stride,
+                              int *bad_ids, hipStream_t stream) {
+    if (!valid_rate(bits, codebook) || !valid_matrix(k, n, 128) || !valid_dtype(ot)) return EXL3_INVAL_PARAMS;
+    if (!count) return EXL3_OK;
+    if (count > 0x7fffffffu || !records || !ids || !out || !aligned(records, 16) || !aligned(ids, 4) ||
+        !aligned(out, dtype_size(ot)) || out_row_stride < k || (bad_ids && !aligned(bad_ids, 4)))
+        return EXL3_INVAL_PARAMS;
+    return from_hip(exl3k::launch_get_rows(records, (int)bits, (int)codebook, k, n, ids, count, out, ot == EXL3_F16,
+                                           out_row_stride, bad_ids, stream));
+}
+
 exl3_status exl3_hip_codebook(const uint16_t *states, size_t count, unsigned codebook, uint16_t *out,
                               hipStream_t stream) {
     if (codebook > 2 || (count && (!states || !out))) return EXL3_INVAL_PARAMS;

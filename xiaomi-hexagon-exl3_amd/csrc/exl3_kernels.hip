@@ -6,11 +6,15 @@
 //                    MFMA columns, v_mfma_f32_16x16x32_f16 accumulates in fp32;
 //                    split-K partials are reduced in fixed order by the last
 //                    workgroup of each 128-column group, which applies H128 and sv.
-//   gemm_kernel      rows > 8: a workgroup decodes one 128x128 record per step into
-//                    LDS (fp16, n-major), streams a 128-row activation tile through
-//                    LDS and runs 16x16x32 f16 MFMAs, fp32 accumulation.
+//   gemm_xprep_kernel, gemm_kernel, gemm_reduce_kernel
+//                    rows > 8: H128(x*su) once in fp16 MFMA-fragment order; a
+//                    workgroup (k split, column group, m-tile) decodes record kb + 1
+//                    into LDS (fp16, swizzled) while v_mfma_f32_32x32x16_f16 runs on
+//                    record kb, fp32 accumulation; split partials are summed in
+//                    fixed order by the reduce kernel, which applies H128 and sv.
 //   decode_kernel    trellis tiles -> row-major fp16, bit-exact (exl3::decode_inner).
 //   reconstruct_kernel original-basis weights, bit-exact (exl3::reconstruct).
+//   get_rows_kernel    GET_ROWS: columns of the original-basis weights (ggml_exl3_get_rows).
 // Reference semantics: src/exl3_codec.cpp, src/exl3-ggml.cpp:51-92.
 #include <hip/hip_runtime.h>
 
@@ -317,6 +321,120 @@ hipError_t launch_reconstruct(const void *src, int rl, const uint16_t *su, const
     case 6: return launch_reconstruct_k<6>(src, rl, su, sv, cb, k, n, first, count, out, stream);
     case 7: return launch_reconstruct_k<7>(src, rl, su, sv, cb, k, n, first, count, out, stream);
     default: return launch_reconstruct_k<8>(src, rl, su, sv, cb, k, n, first, count, out, stream);
+    }
+}
+
+// ============================================================== get_rows
+// GET_ROWS on records (src/exl3-ggml.cpp:19-49).  Workgroup (r, kb) writes
+// out[r][128 kb .. +127] = column c = ids[r] % 128 of the original-basis
+// reconstruct of record (ids[r] / 128, kb) as a 128x128 matrix, fp16-rounded
+// (then widened for F32 output): decode into LDS (fp32), the H128 of each row
+// over n restricted to the operations output c depends on (the same
+// butterflies, in the same order, as the full transform: bit-exact), then the
+// full H128 of that column over k and fp16((w * su) * sv) as exl3::reconstruct.
+// An id outside [0, n) writes a NaN row and sets *bad_ids (if given) to 1.
+template <int K, int CB>
+__global__ __launch_bounds__(256) void get_rows_kernel(const uint8_t *__restrict__ records, size_t k, size_t n,
+                                                       const int32_t *__restrict__ ids, void *__restrict__ out,
+                                                       int out_f16, size_t out_stride, int *__restrict__ bad_ids) {
+    constexpr int P = 129;
+    __shared__ float blk[128 * P];
+    __shared__ float colv[128];
+    const int tid = threadIdx.x;
+    const size_t r = blockIdx.x, kb = blockIdx.y;
+    const int32_t id = ids[r];
+    const size_t o = r * out_stride + kb * 128;
+    if (id < 0 || (size_t)id >= n) {
+        if (tid < 128) {
+            if (out_f16) ((uint16_t *)out)[o + tid] = 0x7e00u;
+            else ((uint32_t *)out)[o + tid] = 0x7fc00000u;
+        }
+        if (tid == 0 && kb == 0 && bad_ids) *bad_ids = 1;
+        return;
+    }
+    const size_t nb = (size_t)id >> 7;
+    const int c = id & 127;
+#pragma unroll 1
+    for (int i = 0; i < 4; ++i) {
+        const int run = tid + 256 * i;
+        const int tile = run >> 4, rc = run & 15;
+        const int cr = rc & 7, h = rc >> 3, tr = tile >> 3, tc = tile & 7;
+        const uint32_t *tp = tile_ptr<K>(records, 1, k, n, kb * 8 + tr, nb * 8 + tc);
+        uint32_t w[RunGeo<K>::NW];
+        load_run_words<K>(tp, cr, h, w);
+        u4 a1, a2;
+        decode_run<K, CB>(w, a1, a2);
+        const uint32_t p1[4] = {a1.x, a1.y, a1.z, a1.w}, p2[4] = {a2.x, a2.y, a2.z, a2.w};
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int r0 = tr * 16 + run_slot_row(h, 2 * v), r1 = tr * 16 + run_slot_row(h, 2 * v + 1);
+            const int cc = tc * 16 + cr;
+            blk[r0 * P + cc] = half_bits_to_float((uint16_t)(p1[v] & 0xffffu));
+            blk[r1 * P + cc] = half_bits_to_float((uint16_t)(p1[v] >> 16));
+            blk[r0 * P + cc + 8] = half_bits_to_float((uint16_t)(p2[v] & 0xffffu));
+            blk[r1 * P + cc + 8] = half_bits_to_float((uint16_t)(p2[v] >> 16));
+        }
+    }
+    __syncthreads();
+    // row tid: after the stage of stride 2^s only positions agreeing with c on
+    // bits 0..s matter; v[m] holds position (m << (s + 1)) | (c & (2^(s+1) - 1))
+    if (tid < 128) {
+        const float *row = blk + tid * P;
+        float v[64];
+#pragma unroll
+        for (int m = 0; m < 64; ++m) {
+            const float a = row[2 * m], b = row[2 * m + 1];
+            v[m] = (c & 1) ? a - b : a + b;
+        }
+#pragma unroll
+        for (int s = 1; s < 7; ++s)
+#pragma unroll
+            for (int m = 0; m < (64 >> s); ++m) v[m] = ((c >> s) & 1) ? v[2 * m] - v[2 * m + 1] : v[2 * m] + v[2 * m + 1];
+        colv[tid] = v[0] * 0.08838834764831844055f;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        float e0 = colv[tid], e1 = colv[tid + 64];
+        h128_wave(e0, e1, tid);
+        const uint8_t *rec = records + (nb * (k >> 7) + kb) * group_bytes(K);
+        const uint16_t *su = (const uint16_t *)(rec + 2048 * K);
+        const float svc = half_bits_to_float(((const uint16_t *)(rec + 2048 * K + 256))[c]);
+        const uint16_t h0 = float_to_half_bits(mul_rn_f32(mul_rn_f32(e0, half_bits_to_float(su[tid])), svc));
+        const uint16_t h1 = float_to_half_bits(mul_rn_f32(mul_rn_f32(e1, half_bits_to_float(su[tid + 64])), svc));
+        if (out_f16) {
+            ((uint16_t *)out)[o + tid] = h0;
+            ((uint16_t *)out)[o + tid + 64] = h1;
+        } else {
+            ((float *)out)[o + tid] = half_bits_to_float(h0);
+            ((float *)out)[o + tid + 64] = half_bits_to_float(h1);
+        }
+    }
+}
+
+template <int K>
+static hipError_t launch_get_rows_k(const void *records, int cb, size_t k, size_t n, const int32_t *ids, size_t count,
+                                    void *out, int out_f16, size_t out_stride, int *bad_ids, hipStream_t stream) {
+    const dim3 grid((unsigned)count, (unsigned)(k / 128)), block(256);
+    const uint8_t *rec = (const uint8_t *)records;
+    switch (cb) {
+    case 0: get_rows_kernel<K, 0><<<grid, block, 0, stream>>>(rec, k, n, ids, out, out_f16, out_stride, bad_ids); break;
+    case 1: get_rows_kernel<K, 1><<<grid, block, 0, stream>>>(rec, k, n, ids, out, out_f16, out_stride, bad_ids); break;
+    default: get_rows_kernel<K, 2><<<grid, block, 0, stream>>>(rec, k, n, ids, out, out_f16, out_stride, bad_ids); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_get_rows(const void *records, int bits, int cb, size_t k, size_t n, const int32_t *ids, size_t count,
+                           void *out, int out_f16, size_t out_stride, int *bad_ids, hipStream_t stream) {
+    switch (bits) {
+    case 1: return launch_get_rows_k<1>(records, cb, k, n, ids, count, out, out_f16, out_stride, bad_ids, stream);
+    case 2: return launch_get_rows_k<2>(records, cb, k, n, ids, count, out, out_f16, out_stride, bad_ids, stream);
+    case 3: return launch_get_rows_k<3>(records, cb, k, n, ids, count, out, out_f16, out_stride, bad_ids, stream);
+    case 4: return launch_get_rows_k<4>(records, cb, k, n, ids, count, out, out_f16, out_stride, bad_ids, stream);
+    case 5: return launch_get_rows_k<5>(records, cb, k, n, ids, count, out, out_f16, out_stride, bad_ids, stream);
+    case 6: return launch_get_rows_k<6>(records, cb, k, n, ids, count, out, out_f16, out_stride, bad_ids, stream);
+    case 7: return launch_get_rows_k<7>(records, cb, k, n, ids, count, out, out_f16, out_stride, bad_ids, stream);
+    default: return launch_get_rows_k<8>(records, cb, k, n, ids, count, out, out_f16, out_stride, bad_ids, stream);
     }
 }
 

@@ -46,6 +46,8 @@ hipError_t launch_decode(const void *src, int records_layout, int bits, int cb, 
 hipError_t launch_reconstruct(const void *src, int records_layout, const uint16_t *su, const uint16_t *sv,
                               int bits, int cb, size_t k, size_t n, size_t first, size_t count, uint16_t *out,
                               hipStream_t stream);
+hipError_t launch_get_rows(const void *records, int bits, int cb, size_t k, size_t n, const int32_t *ids, size_t count,
+                           void *out, int out_f16, size_t out_stride, int *bad_ids, hipStream_t stream);
 hipError_t launch_codebook(const uint16_t *states, size_t count, int cb, uint16_t *out, hipStream_t stream);
 hipError_t launch_hadamard(float *values, size_t count, hipStream_t stream);
 hipError_t launch_pack_records(const uint16_t *packed, const uint16_t *su, const uint16_t *sv, int bits, size_t k,

@@ -18,8 +18,8 @@ LAYOUT_UPSTREAM_TILES, LAYOUT_RECORDS = 0, 1
 EXPORTS = [
     "exl3_hip_version", "exl3_hip_status_string", "exl3_hip_gemv_max_rows", "exl3_hip_supports_mul_mat",
     "exl3_hip_mul_mat_workspace_bytes", "exl3_hip_workspace_init", "exl3_hip_mul_mat", "exl3_hip_decode",
-    "exl3_hip_reconstruct", "exl3_hip_codebook", "exl3_hip_hadamard128", "exl3_hip_pack_records",
-    "exl3_hip_validate_records",
+    "exl3_hip_reconstruct", "exl3_hip_get_rows", "exl3_hip_codebook", "exl3_hip_hadamard128",
+    "exl3_hip_pack_records", "exl3_hip_validate_records",
 ]
 
 
@@ -52,6 +52,8 @@ def load(path=LIB_PATH):
     L.exl3_hip_decode.argtypes = [vp, i, u, u, sz, sz, sz, sz, vp, st]
     L.exl3_hip_reconstruct.restype = i
     L.exl3_hip_reconstruct.argtypes = [vp, i, vp, vp, u, u, sz, sz, sz, sz, vp, st]
+    L.exl3_hip_get_rows.restype = i
+    L.exl3_hip_get_rows.argtypes = [vp, u, u, sz, sz, vp, sz, vp, i, sz, vp, st]
     L.exl3_hip_codebook.restype = i
     L.exl3_hip_codebook.argtypes = [vp, sz, u, vp, st]
     L.exl3_hip_hadamard128.restype = i
@@ -136,6 +138,23 @@ def reconstruct(src, bits, k, n, su=None, sv=None, codebook=CB_MUL1, layout=LAYO
         out = torch.empty((k, count), dtype=torch.int16, device=src.device)
     _check(lib().exl3_hip_reconstruct(_ptr(src), layout, _ptr(su), _ptr(sv), bits, codebook, k, n, first, count,
                                       _ptr(out), _stream(stream)), "reconstruct")
+    return out
+
+
+def get_rows(records, bits, k, n, ids, codebook=CB_MUL1, out_dtype=None, out=None, bad_ids=None, stream=None):
+    """GET_ROWS (ggml_exl3_get_rows): out[r] = column ids[r] of the original-basis
+    weight, [count, k] fp32 (ggml's dst type) or fp16.  ids: int32 CUDA tensor.
+    bad_ids: optional int32 CUDA tensor of one element, set to 1 when an id is
+    outside [0, n) (that row is NaN)."""
+    import torch
+    assert ids.dtype == torch.int32 and ids.is_contiguous()
+    count = ids.numel()
+    if out is None:
+        out = torch.empty((count, k), dtype=out_dtype or torch.float32, device=ids.device)
+    assert out.dim() == 2 and out.stride(1) == 1 and out.dtype in (torch.float16, torch.float32)
+    ot = F16 if out.dtype == torch.float16 else F32
+    _check(lib().exl3_hip_get_rows(_ptr(records), bits, codebook, k, n, _ptr(ids), count, _ptr(out), ot,
+                                   out.stride(0), _ptr(bad_ids), _stream(stream)), "get_rows")
     return out
 
 
