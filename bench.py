@@ -4,7 +4,10 @@ Headline (the `value`): decode-time GEMV, k=14336 in x n=4096 out at 4 bits per
 weight (mul1 codebook), batch 1, fp16 activations N(0,1), fused su/H128/sv --
 algorithmic HBM GB/s = (packed trellis + su + sv + x + y bytes) / time.
 Also measured in the same run: batch 2/4/8, a seeded 8-request admission trace
-(active rows uniform in 1..8 per step) and the M=512 prefill GEMM (TFLOP/s).
+(active rows uniform in 1..8 per step), the M=512 prefill GEMM (TFLOP/s), the
+k=2048 x n=6144 layer at batch 1, the projection set of the 2B hybrid model at
+batch 8 (mixed 3/4/6 bits), the dequant-only sweep over that model's 151 weight
+matrices (mixed 2..6 bits) and GET_ROWS of 8 tokens on a vocabulary-head shard.
 
 Every step uses the next of 18 distinct copies of the weights (> 512 MB) so the
 256 MB Infinity Cache cannot serve repeats.  Inputs are resident in HBM before
@@ -45,6 +48,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-gemv", action="store_true", help="headline GEMV only (for profiling)")
     ap.add_argument("--only-gemm", action="store_true", help="M=512 GEMM only (for profiling)")
+    ap.add_argument("--no-extra", action="store_true", help="skip the C1/C2/C4/GET_ROWS lines")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only time a plain device copy of COPY_BYTES (scales the HBM byte counters)")
     return ap.parse_args()
@@ -189,6 +193,9 @@ def main():
         extra["gemm_m512"] = {"tflops": round(tflops, 1), "call_us": round(msg * 1e3, 1),
                               "frac_mfma": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
 
+    if not args.only_gemv and not args.no_extra:
+        extra.update(extra_configs(amd, torch, np, synth, stream, args))
+
     traffic = None
     tfile = ROOT / "profiles" / "traffic_gemv_k14336_n4096_b1.json"
     if tfile.exists():
@@ -226,6 +233,131 @@ def main():
 
 def xs8_slice(xs, r):
     return xs[8][:r]
+
+
+def graph_time(torch, stream, fn, per_graph, replays=3):
+    """Mean ms of one fn() call: a HIP graph holding per_graph calls (fn may
+    rotate through weight copies) replayed `replays` times between HIP events."""
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(per_graph):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s_ev.record(stream)
+    for _ in range(replays):
+        g.replay()
+    e_ev.record(stream)
+    torch.cuda.synchronize()
+    return s_ev.elapsed_time(e_ev) / (replays * per_graph)
+
+
+def c2_matrices():
+    """The 151 weight matrices of the 2B hybrid model (k in, n out)."""
+    mats = []
+    for _ in range(24):
+        mats += [(2048, 6144), (2048, 6144), (6144, 2048)]      # gate, up, down
+    for _ in range(6):
+        mats += [(2048, 2048), (2048, 512), (2048, 512), (2048, 2048)]   # q, k, v, o
+    for _ in range(18):
+        mats += [(2048, 2048), (2048, 2048), (2048, 512)]       # linear-attention projections
+    mats.append((2048, 151936))                                  # vocabulary head
+    return mats
+
+
+def c2_bits(np, synth, mats):
+    """Bits per matrix from {2..6} by seed, redrawn until the weight-weighted mean is <= 5.0."""
+    w = np.array([k * n for k, n in mats], dtype=np.float64)
+    for attempt in range(1000):
+        b = (synth.splitmix64(2222 + attempt, len(mats)) % np.uint64(5)).astype(int) + 2
+        if float(np.sum(w * b) / np.sum(w)) <= 5.0:
+            return b
+    raise RuntimeError("no bit draw met the 5.0 bpw bound")
+
+
+def extra_configs(amd, torch, np, synth, stream, args):
+    out = {}
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev)
+
+    def rand_u16(seed, count):
+        g.manual_seed(seed)
+        return torch.randint(-32768, 32768, (count,), generator=g, device=dev, dtype=torch.int32).to(torch.int16)
+
+    def records(seed, k, n, bits):
+        p = rand_u16(seed, k * n * bits // 16)
+        su = torch.where(rand_u16(seed + 1, k) < 0, -1.0, 1.0).to(torch.float16)
+        sv = (torch.where(rand_u16(seed + 2, n) < 0, -1.0, 1.0) *
+              (0.5 + (rand_u16(seed + 3, n).float() + 32768) / 65536) / (k ** 0.5)).to(torch.float16)
+        return amd.pack_records(p, su, sv, bits, k, n)
+
+    # C1: k=2048 in x n=6144 out, 4 bits, batch 1 (48 weight copies, 302 MB: past the 256 MB MALL)
+    k, n, bits = 2048, 6144, 4
+    copies = [records(100 + i, k, n, bits) for i in range(48)]
+    x = torch.from_numpy(synth.activations(1100, 1, k)).to(dev)
+    y = torch.empty((1, n), dtype=torch.float16, device=dev)
+    ws = amd.new_workspace(k, n, 1)
+    it = iter(range(1 << 30))
+    ms = graph_time(torch, stream, lambda: amd.mul_mat(copies[next(it) % 48], bits, k, n, x, y=y, workspace=ws), 96)
+    out["c1_gemv_k2048_n6144_b1"] = {"gbps": round(algo_bytes(k, n, bits, 1) / (ms * 1e-3) / 1e9, 1),
+                                     "call_us": round(ms * 1e3, 2), "frac_hbm": round(
+                                         algo_bytes(k, n, bits, 1) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                                     "note": "graph replay, 48 weight copies"}
+    del copies
+
+    # C4: projection set of one decoder layer at batch 8, mixed bits, x ~ N(0, sigma 0.5)
+    proj = [("q", 2048, 2048, 6), ("k", 2048, 512, 6), ("v", 2048, 512, 6), ("o", 2048, 2048, 6),
+            ("gate", 2048, 6144, 4), ("up", 2048, 6144, 4), ("down", 6144, 2048, 3)]
+    sets = [[records(400 + 10 * c + i, kk, nn, bb) for i, (_, kk, nn, bb) in enumerate(proj)] for c in range(12)]
+    xs = {kk: torch.from_numpy(synth.activations(4000 + kk, 8, kk, sigma=0.5)).to(dev) for kk in (2048, 6144)}
+    ys = {nn: torch.empty((8, nn), dtype=torch.float16, device=dev) for nn in (512, 2048, 6144)}
+    ws4 = torch.zeros(max(amd.workspace_bytes(kk, nn, 8) for _, kk, nn, _ in proj), dtype=torch.uint8, device=dev)
+    set_bytes = sum(algo_bytes(kk, nn, bb, 8) for _, kk, nn, bb in proj)
+    cnt = iter(range(1 << 30))
+
+    def layer():
+        c = next(cnt) % 12
+        for i, (_, kk, nn, bb) in enumerate(proj):
+            amd.mul_mat(sets[c][i], bb, kk, nn, xs[kk], y=ys[nn], workspace=ws4)
+    ms = graph_time(torch, stream, layer, 24)
+    out["c4_projection_set_b8"] = {"gbps": round(set_bytes / (ms * 1e-3) / 1e9, 1), "layer_us": round(ms * 1e3, 1),
+                                   "frac_hbm": round(set_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                                   "bits": {nm: bb for nm, _, _, bb in proj}, "x_sigma": 0.5,
+                                   "note": "graph replay of 7 calls per layer, 12 copies of the set (> 256 MB)"}
+    del sets
+
+    # C2: dequant-only sweep of the 151 matrices (upstream tile layout -> fp16), bit-exactness in tests
+    mats = c2_matrices()
+    bits_c2 = c2_bits(np, synth, mats)
+    packed = [rand_u16(9000 + i, k2 * n2 * int(b2) // 16) for i, ((k2, n2), b2) in enumerate(zip(mats, bits_c2))]
+    dst = torch.empty(max(k2 * n2 for k2, n2 in mats), dtype=torch.int16, device=dev)
+
+    def sweep():
+        for (k2, n2), b2, p2 in zip(mats, bits_c2, packed):
+            amd.decode(p2, int(b2), k2, n2, codebook=CB, out=dst[: k2 * n2].view(k2, n2))
+    ms = graph_time(torch, stream, sweep, 1, replays=3)
+    c2_bytes = sum(k2 * n2 * int(b2) // 8 + 2 * k2 * n2 for (k2, n2), b2 in zip(mats, bits_c2))
+    wsum = sum(k2 * n2 for k2, n2 in mats)
+    out["c2_dequant_sweep"] = {"gbps": round(c2_bytes / (ms * 1e-3) / 1e9, 1), "sweep_ms": round(ms, 3),
+                               "frac_hbm": round(c2_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                               "matrices": len(mats), "weights": wsum,
+                               "mean_bpw": round(float(sum(k2 * n2 * int(b2) for (k2, n2), b2 in zip(mats, bits_c2)) / wsum), 3),
+                               "bytes": c2_bytes}
+    del packed, dst
+
+    # GET_ROWS: 8 token ids on a 1/8 vocabulary-head shard (k=2048 hidden, 6 bits)
+    k, n, bits = 2048, 151936 // 8 // 128 * 128, 6
+    rec = records(777, k, n, bits)
+    ids = torch.tensor([5, n // 2, n - 1, 1000, 77, 4096, 18000 % n, 123], dtype=torch.int32, device=dev)
+    rows = torch.empty((8, k), dtype=torch.float32, device=dev)
+    ms = graph_time(torch, stream, lambda: amd.get_rows(rec, bits, k, n, ids, out=rows), 50)
+    rbytes = 8 * (k // 128) * (2048 * bits + 512)
+    out["get_rows_head_shard"] = {"call_us": round(ms * 1e3, 2), "tokens": 8, "k": k, "n": n, "bits": bits,
+                                  "record_gbps": round(rbytes / (ms * 1e-3) / 1e9, 1)}
+    return out
 
 
 def cpu_baseline(np, synth):
