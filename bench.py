@@ -147,7 +147,7 @@ def main():
         return start.elapsed_time(stop) / (reps * COPIES), reps * COPIES
 
     if args.only_gemm:
-        msg, n = timed(512, x512, max(10, args.steps // 10), max(3, args.warmup // 4))
+        msg, n = timed(512, x512, max(36, args.steps // 2), max(18, args.warmup))
         print(json.dumps({"gemm_m512_us": round(msg * 1e3, 2), "launches": n,
                           "tflops": round(2.0 * 512 * K_IN * N_OUT / (msg * 1e-3) / 1e12, 1)}), flush=True)
         return
@@ -186,8 +186,8 @@ def main():
         extra["gemv_admission_trace"] = {"gbps": round(tbytes / (tms * 1e-3) / 1e9, 1),
                                          "mean_rows": float(np.mean(trace)), "steps": args.steps}
         # prefill GEMM, M = 512
-        gsteps = max(10, args.steps // 10)
-        msg, _ = timed(512, x512, gsteps, max(3, args.warmup // 4))
+        gsteps = max(36, args.steps // 2)
+        msg, _ = timed(512, x512, gsteps, max(18, args.warmup))
         flops = 2.0 * 512 * K_IN * N_OUT
         tflops = flops / (msg * 1e-3) / 1e12
         extra["gemm_m512"] = {"tflops": round(tflops, 1), "call_us": round(msg * 1e3, 1),
