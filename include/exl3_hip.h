@@ -26,6 +26,8 @@
  *   exl3_hip_validate_records <- ggml_validate_row_data EXL3 case
  *                            patches/llama-exl3.patch:327-338
  *   exl3_hip_supports_mul_mat <- supports_op predicates patches/llama-exl3.patch:81-84,225-235
+ *   exl3_hip_model_*      <- exl3::Model src/exl3_model.cpp:79-187 (include/exl3_model.h),
+ *                            for C callers; the C++ class is include/exl3_model.h
  */
 #ifndef EXL3_HIP_H
 #define EXL3_HIP_H
@@ -144,6 +146,35 @@ exl3_status exl3_hip_pack_records(const uint16_t *packed, const uint16_t *su, co
  * 0 otherwise; EXL3_INVAL_PARAMS when nbytes is not a whole number of records. */
 exl3_status exl3_hip_validate_records(const void *records, size_t nbytes, unsigned bits, int *result,
                                       hipStream_t stream);
+
+/* ---- deployment model reader (exl3::Model, src/exl3_model.cpp:79-187) ----
+ * A model directory holds model.safetensors and hexagon-exl3.json; it is
+ * validated as the reference validates it.  Host memory maps the file; the
+ * embedding and the record upload use the current HIP device. */
+typedef struct exl3_model exl3_model;
+
+/* NULL when the directory is missing or malformed; the reason is copied into
+ * error (NUL-terminated, at most error_bytes - 1 characters) when given. */
+exl3_model *exl3_hip_model_open(const char *directory, char *error, size_t error_bytes);
+void exl3_hip_model_close(exl3_model *model);
+size_t exl3_hip_model_tensor_count(const exl3_model *model);
+size_t exl3_hip_model_payload_bytes(const exl3_model *model);
+size_t exl3_hip_model_hidden_size(const exl3_model *model);
+size_t exl3_hip_model_vocab_size(const exl3_model *model);
+double exl3_hip_model_bits_per_weight(const exl3_model *model);
+/* out (host) = hidden_size fp16 bits of token's tied embedding, bit-exact with
+ * exl3::Model::embedding; EXL3_INVAL_PARAMS when token >= vocab_size. */
+exl3_status exl3_hip_model_embedding(const exl3_model *model, uint32_t token, uint16_t *out);
+/* EXL3 matrices of the model (every <prefix>.trellis with its .suh/.svh), in name order */
+size_t exl3_hip_model_matrix_count(const exl3_model *model);
+exl3_status exl3_hip_model_matrix(const exl3_model *model, size_t index, char *name, size_t name_bytes,
+                                  unsigned *bits, unsigned *codebook, size_t *k, size_t *n);
+/* device bytes of matrix index's group records (0 for a bad index) */
+size_t exl3_hip_model_record_bytes(const exl3_model *model, size_t index);
+/* packs matrix index into group records at device pointer records (16-byte
+ * aligned, exl3_hip_model_record_bytes long), ready for exl3_hip_mul_mat;
+ * returns when they are complete.  k and n must be multiples of 128. */
+exl3_status exl3_hip_model_upload_records(const exl3_model *model, size_t index, void *records, hipStream_t stream);
 
 #ifdef __cplusplus
 }

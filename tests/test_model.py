@@ -1,0 +1,182 @@
+"""exl3::Model, the deployment-model reader (src/exl3_model.cpp:79-187), through
+the C-ABI: the reference's own reader test (tests/test_model_reader.cpp:23-73)
+and further malformed inputs on the CPU; embeddings and record uploads on the GPU
+against the oracle."""
+import copy
+import struct
+
+import numpy as np
+import pytest
+
+import conftest
+import synth
+from model_files import random_model, reference_case, write_model
+
+
+def amd_lib():
+    return conftest.load_amd()
+
+
+def open_or_reason(d):
+    amd = amd_lib()
+    try:
+        return amd.Model(d), None
+    except amd.Exl3Error as e:
+        return None, str(e)
+
+
+def test_reference_reader_case_opens(tmp_path):
+    header, data, manifest = reference_case()
+    write_model(tmp_path, header, data, manifest)
+    m, why = open_or_reason(tmp_path)
+    assert m is not None, why
+    with m:
+        # test_model_reader.cpp:49
+        assert m.tensor_count == 4 and m.payload_bytes == 8708
+        assert m.hidden_size == 128 and m.vocab_size == 128
+        assert m.bits_per_weight == pytest.approx(8708 * 8 / 16384)
+        assert m.matrices() == [("lm_head", 4, 2, 128, 128)]
+
+
+def mutations():
+    """(name, mutate(header, data, manifest)) -> each must be rejected"""
+    def set_(path, value, which):
+        def f(h, d, m):
+            tgt = {"h": h, "m": m}[which]
+            for key in path[:-1]:
+                tgt = tgt[key]
+            tgt[path[-1]] = value
+            return h, d, m
+        return f
+    def drop(path, which):
+        def f(h, d, m):
+            tgt = {"h": h, "m": m}[which]
+            for key in path[:-1]:
+                tgt = tgt[key]
+            del tgt[path[-1]]
+            return h, d, m
+        return f
+    def truncate(h, d, m):
+        return h, d[:-1], m
+    def add_mcg(h, d, m):
+        h["lm_head.mcg"] = {"dtype": "I32", "shape": [], "data_offsets": [8708, 8712]}
+        m["weight_payload_bytes"] = 8712
+        return h, d + struct.pack("<I", 0xCBAC1FED), m
+    def bad_mul1(h, d, m):
+        d = bytearray(d)
+        d[8704:8708] = struct.pack("<I", 0x12345678)
+        return h, d, m
+    return [
+        # the four rejections of tests/test_model_reader.cpp:67-72
+        ("budget: parameter count 1", set_(["reference_parameter_count"], 1, "m")),
+        ("overlapping spans", set_(["lm_head.suh", "data_offsets"], [8190, 8446], "h")),
+        ("negative dimension", set_(["lm_head.suh", "shape"], [-128], "h")),
+        ("truncated payload", truncate),
+        # further checks of src/exl3_model.cpp:79-156
+        ("zero dimension", set_(["lm_head.suh", "shape"], [0], "h")),
+        ("real dimension", set_(["lm_head.suh", "shape"], [128.0], "h")),
+        ("unsupported dtype", set_(["lm_head.suh", "dtype"], "F64", "h")),
+        ("span length != shape", set_(["lm_head.svh", "shape"], [64], "h")),
+        ("offset pair of 3", set_(["lm_head.svh", "data_offsets"], [8448, 8704, 8704], "h")),
+        ("gap in payload", set_(["lm_head.svh", "data_offsets"], [8450, 8706], "h")),
+        ("payload bytes mismatch", set_(["weight_payload_bytes"], 8700, "m")),
+        ("manifest format", set_(["format"], "exl3", "m")),
+        ("manifest version", set_(["version"], 2, "m")),
+        ("kv cache", set_(["kv_cache"], "q8", "m")),
+        ("embedding type", set_(["input_embedding", "type"], "linear", "m")),
+        ("token axis", set_(["input_embedding", "token_axis"], 0, "m")),
+        ("hidden size not /128", set_(["input_embedding", "hidden_size"], 96, "m")),
+        ("missing source tensor", set_(["input_embedding", "source"], "head", "m")),
+        ("missing manifest key", drop(["kv_cache"], "m")),
+        ("trellis dtype", set_(["lm_head.trellis", "dtype"], "F16", "h")),
+        ("trellis shape", set_(["lm_head.trellis", "shape"], [8, 4, 128], "h")),
+        ("ambiguous codebook", add_mcg),
+        ("mul1 multiplier", bad_mul1),
+    ]
+
+
+@pytest.mark.parametrize("name,mutate", mutations(), ids=[m[0] for m in mutations()])
+def test_malformed_models_rejected(tmp_path, name, mutate):
+    header, data, manifest = reference_case()
+    header, data, manifest = mutate(copy.deepcopy(header), bytes(data), copy.deepcopy(manifest))
+    write_model(tmp_path, header, data, manifest)
+    m, why = open_or_reason(tmp_path)
+    assert m is None, name
+    assert why
+
+
+def test_header_length_and_missing_files(tmp_path):
+    header, data, manifest = reference_case()
+    write_model(tmp_path, header, data, manifest)
+    raw = bytearray((tmp_path / "model.safetensors").read_bytes())
+    raw[0:8] = struct.pack("<Q", len(raw))            # header longer than the file
+    (tmp_path / "model.safetensors").write_bytes(bytes(raw))
+    assert open_or_reason(tmp_path)[0] is None
+    write_model(tmp_path, header, data, manifest)
+    (tmp_path / "hexagon-exl3.json").unlink()
+    assert open_or_reason(tmp_path)[0] is None
+    assert open_or_reason(tmp_path / "absent")[0] is None
+
+
+def test_codebook_markers_and_matrix_inventory(tmp_path):
+    mats = [("model.layers.0.mlp.down_proj", 256, 128, 3, 0), ("model.layers.0.mlp.gate_proj", 128, 256, 5, 1),
+            ("lm_head", 128, 384, 4, 2)]     # 4.0 bits per weight on average: within the 5.0 budget
+    header, data, manifest, _ = random_model(90, mats, "lm_head")
+    write_model(tmp_path, header, data, manifest)
+    m, why = open_or_reason(tmp_path)
+    assert m is not None, why
+    with m:
+        assert m.tensor_count == 3 * 3 + 2            # the 3inst matrix has no marker
+        assert sorted(m.matrices()) == sorted((p, b, c, k, n) for p, k, n, b, c in mats)
+        assert m.hidden_size == 128 and m.vocab_size == 384
+
+
+# ---- GPU ------------------------------------------------------------------------
+
+@pytest.mark.gpu
+def test_embedding_known_answer(tmp_path, amd, oracle):
+    # test_model_reader.cpp:50-59
+    header, data, manifest = reference_case()
+    write_model(tmp_path, header, data, manifest)
+    with amd.Model(tmp_path) as m:
+        row0, row1 = m.embedding(0), m.embedding(1)
+        assert np.array_equal(row0, m.embedding(0))
+        code = oracle.L.orc_half_to_float(oracle.L.orc_decode_codebook(0, 2))
+        assert row0[0] == oracle.L.orc_float_to_half(code * 128)
+        assert np.all(row0[1:].view(np.float16) == 0) and np.all(row1.view(np.float16) == 0)
+        with pytest.raises(amd.Exl3Error):
+            m.embedding(128)
+
+
+@pytest.mark.gpu
+def test_embedding_matches_reconstruct_across_groups(tmp_path, amd, oracle):
+    # a 4-bit mcg head of 20 token groups: more groups than the 16-entry cache holds
+    k, n = 256, 128 * 20
+    header, data, manifest, parts = random_model(91, [("lm_head", k, n, 4, 1)], "lm_head")
+    write_model(tmp_path, header, data, manifest)
+    p, su, sv = parts["lm_head"]
+    full = oracle.reconstruct(p, su, sv, k, n, 4, 1)
+    tokens = [0, 5, 130, 127, 2559, 1000] + [128 * g + g for g in range(20)] + [0, 5, 2559]
+    with amd.Model(tmp_path) as m:
+        for t in tokens:
+            assert np.array_equal(m.embedding(t), full[:, t]), t
+
+
+@pytest.mark.gpu
+def test_upload_records_feed_the_layer(tmp_path, amd, oracle):
+    import torch
+    from gpu_util import assert_layer_close
+    mats = [("model.layers.0.mlp.down_proj", 256, 128, 3, 0), ("lm_head", 128, 384, 4, 2)]
+    header, data, manifest, parts = random_model(92, mats, "lm_head")
+    write_model(tmp_path, header, data, manifest)
+    with amd.Model(tmp_path) as m:
+        inventory = m.matrices()
+        for idx, (prefix, bits, cb, k, n) in enumerate(inventory):
+            p, su, sv = parts[prefix]
+            rec = m.upload_records(idx)
+            torch.cuda.synchronize()
+            want = synth.pack_records(p, su, sv, bits).view(np.uint8)
+            assert np.array_equal(rec.cpu().numpy(), want), prefix
+            x = synth.activations(93 + idx, 3, k)
+            y = amd.mul_mat(rec, bits, k, n, torch.from_numpy(x).cuda(), codebook=cb).cpu().numpy()
+            assert_layer_close(y, oracle.mul_mat(want, bits, cb, k, n, x), what=prefix)

@@ -20,6 +20,10 @@ EXPORTS = [
     "exl3_hip_mul_mat_workspace_bytes", "exl3_hip_workspace_init", "exl3_hip_mul_mat", "exl3_hip_decode",
     "exl3_hip_reconstruct", "exl3_hip_get_rows", "exl3_hip_codebook", "exl3_hip_hadamard128",
     "exl3_hip_pack_records", "exl3_hip_validate_records",
+    "exl3_hip_model_open", "exl3_hip_model_close", "exl3_hip_model_tensor_count", "exl3_hip_model_payload_bytes",
+    "exl3_hip_model_hidden_size", "exl3_hip_model_vocab_size", "exl3_hip_model_bits_per_weight",
+    "exl3_hip_model_embedding", "exl3_hip_model_matrix_count", "exl3_hip_model_matrix", "exl3_hip_model_record_bytes",
+    "exl3_hip_model_upload_records",
 ]
 
 
@@ -54,6 +58,24 @@ def load(path=LIB_PATH):
     L.exl3_hip_reconstruct.argtypes = [vp, i, vp, vp, u, u, sz, sz, sz, sz, vp, st]
     L.exl3_hip_get_rows.restype = i
     L.exl3_hip_get_rows.argtypes = [vp, u, u, sz, sz, vp, sz, vp, i, sz, vp, st]
+    L.exl3_hip_model_open.restype = vp
+    L.exl3_hip_model_open.argtypes = [ctypes.c_char_p, ctypes.c_char_p, sz]
+    L.exl3_hip_model_close.restype = None
+    L.exl3_hip_model_close.argtypes = [vp]
+    for fn in ("tensor_count", "payload_bytes", "hidden_size", "vocab_size", "matrix_count"):
+        getattr(L, "exl3_hip_model_" + fn).restype = sz
+        getattr(L, "exl3_hip_model_" + fn).argtypes = [vp]
+    L.exl3_hip_model_bits_per_weight.restype = ctypes.c_double
+    L.exl3_hip_model_bits_per_weight.argtypes = [vp]
+    L.exl3_hip_model_embedding.restype = i
+    L.exl3_hip_model_embedding.argtypes = [vp, ctypes.c_uint32, vp]
+    L.exl3_hip_model_matrix.restype = i
+    L.exl3_hip_model_matrix.argtypes = [vp, sz, ctypes.c_char_p, sz, ctypes.POINTER(u), ctypes.POINTER(u),
+                                        ctypes.POINTER(sz), ctypes.POINTER(sz)]
+    L.exl3_hip_model_record_bytes.restype = sz
+    L.exl3_hip_model_record_bytes.argtypes = [vp, sz]
+    L.exl3_hip_model_upload_records.restype = i
+    L.exl3_hip_model_upload_records.argtypes = [vp, sz, vp, st]
     L.exl3_hip_codebook.restype = i
     L.exl3_hip_codebook.argtypes = [vp, sz, u, vp, st]
     L.exl3_hip_hadamard128.restype = i
@@ -156,6 +178,70 @@ def get_rows(records, bits, k, n, ids, codebook=CB_MUL1, out_dtype=None, out=Non
     _check(lib().exl3_hip_get_rows(_ptr(records), bits, codebook, k, n, _ptr(ids), count, _ptr(out), ot,
                                    out.stride(0), _ptr(bad_ids), _stream(stream)), "get_rows")
     return out
+
+
+class Model:
+    """exl3::Model (src/exl3_model.cpp:79-187) through the C-ABI: the deployment
+    reader of a directory with model.safetensors and hexagon-exl3.json.  Raises
+    Exl3Error (status INVAL_PARAMS) with the reader's reason when the model is
+    malformed."""
+
+    def __init__(self, directory):
+        err = ctypes.create_string_buffer(512)
+        h = lib().exl3_hip_model_open(str(directory).encode(), err, len(err))
+        if not h:
+            raise Exl3Error(1, "model_open: " + err.value.decode(errors="replace"))
+        self._h = h
+
+    def close(self):
+        if self._h:
+            lib().exl3_hip_model_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    tensor_count = property(lambda self: lib().exl3_hip_model_tensor_count(self._h))
+    payload_bytes = property(lambda self: lib().exl3_hip_model_payload_bytes(self._h))
+    hidden_size = property(lambda self: lib().exl3_hip_model_hidden_size(self._h))
+    vocab_size = property(lambda self: lib().exl3_hip_model_vocab_size(self._h))
+    bits_per_weight = property(lambda self: lib().exl3_hip_model_bits_per_weight(self._h))
+
+    def embedding(self, token):
+        """fp16 bits (numpy uint16 [hidden_size]) of token's tied embedding"""
+        import numpy as np
+        out = np.zeros(self.hidden_size, dtype=np.uint16)
+        _check(lib().exl3_hip_model_embedding(self._h, token, out.ctypes.data_as(ctypes.c_void_p)), "model_embedding")
+        return out
+
+    def matrices(self):
+        """[(prefix, bits, codebook, k, n)] of every EXL3 matrix, in name order"""
+        out = []
+        for idx in range(lib().exl3_hip_model_matrix_count(self._h)):
+            name = ctypes.create_string_buffer(1024)
+            b, c = ctypes.c_uint(), ctypes.c_uint()
+            kk, nn = ctypes.c_size_t(), ctypes.c_size_t()
+            _check(lib().exl3_hip_model_matrix(self._h, idx, name, len(name), ctypes.byref(b), ctypes.byref(c),
+                                               ctypes.byref(kk), ctypes.byref(nn)), "model_matrix")
+            out.append((name.value.decode(), b.value, c.value, kk.value, nn.value))
+        return out
+
+    def upload_records(self, index, device="cuda", stream=None):
+        """uint8 CUDA tensor of matrix index's group records (for mul_mat)"""
+        import torch
+        nbytes = lib().exl3_hip_model_record_bytes(self._h, index)
+        rec = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        _check(lib().exl3_hip_model_upload_records(self._h, index, _ptr(rec), _stream(stream)), "model_upload_records")
+        return rec
 
 
 def codebook_values(states, codebook, out=None, stream=None):
