@@ -187,18 +187,41 @@ __device__ __forceinline__ void h128_lds(float *v, int rows, int stride, int tid
     __syncthreads();
 }
 
+// Value of lane lane ^ S (S = 1, 2, 4, 8) inside each row of 16 lanes, by DPP
+// (row_ror:n gives lane i the value of lane (i - n) mod 16).
+template <int S>
+__device__ __forceinline__ float dpp_xor(float v) {
+    const int iv = __float_as_int(v);
+    if constexpr (S == 1) {
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xF, 0xF, false));  // quad_perm 1,0,3,2
+    } else if constexpr (S == 2) {
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xF, 0xF, false));  // quad_perm 2,3,0,1
+    } else if constexpr (S == 4) {
+        // lanes 0-3 and 8-11 of the row (banks 0, 2) read lane + 4 (row_ror:12),
+        // lanes 4-7 and 12-15 (banks 1, 3) read lane - 4 (row_ror:4)
+        const int t = __builtin_amdgcn_update_dpp(iv, iv, 0x12C, 0xF, 0x5, false);
+        return __int_as_float(__builtin_amdgcn_update_dpp(t, iv, 0x124, 0xF, 0xA, false));
+    } else {
+        static_assert(S == 8, "dpp_xor: S in 1, 2, 4, 8");
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, iv, 0x128, 0xF, 0xF, false));  // row_ror:8
+    }
+}
+
 // H128 of one 128-block held by a wave: lane l owns element l in v0 and element
 // l + 64 in v1.  Stages 1..32 pair lanes l and l ^ step, stage 64 pairs v0/v1;
 // each butterfly is (a + b, a - b) with a the lower index, in the reference's
 // stage order (src/exl3_codec.cpp:153-165), then the 1/sqrt(128) scale.  Lane
-// exchanges use ds_swizzle (xor 1..16 inside 32-lane halves) and one ds_bpermute
-// (xor 32); each butterfly is one fma with a +-1 lane sign, exact like a +- b.
+// exchanges use DPP (xor 1..8 inside 16-lane rows), ds_swizzle (xor 16) and
+// ds_bpermute (xor 32); each butterfly is one fma with a +-1 lane sign, exact
+// like a +- b.
 template <int STEP>
 __device__ __forceinline__ float lane_xor(float v, int bperm_addr32) {
     if constexpr (STEP == 32) {
         return __int_as_float(__builtin_amdgcn_ds_bpermute(bperm_addr32, __float_as_int(v)));
-    } else {
+    } else if constexpr (STEP == 16) {
         return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (STEP << 10)));
+    } else {
+        return dpp_xor<STEP>(v);  // VALU, no LDS round trip
     }
 }
 

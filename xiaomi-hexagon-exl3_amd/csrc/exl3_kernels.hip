@@ -844,26 +844,6 @@ __host__ __device__ inline size_t gemm_xh_offset(int row, int kb, int e, int kbs
     const int ln = (row & 31) + 32 * (kk >> 3);
     return ((((size_t)(row >> 5) * kbs + kb) * 8 + ks) * 64 + ln) * 8 + (kk & 7);
 }
-// Value of lane lane ^ S (S = 1, 2, 4, 8) inside each row of 16 lanes, by DPP
-// (row_ror:n gives lane i the value of lane (i - n) mod 16).
-template <int S>
-__device__ __forceinline__ float dpp_xor(float v) {
-    const int iv = __float_as_int(v);
-    if constexpr (S == 1) {
-        return __int_as_float(__builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xF, 0xF, false));  // quad_perm 1,0,3,2
-    } else if constexpr (S == 2) {
-        return __int_as_float(__builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xF, 0xF, false));  // quad_perm 2,3,0,1
-    } else if constexpr (S == 4) {
-        // lanes 0-3 and 8-11 of the row (banks 0, 2) read lane + 4 (row_ror:12),
-        // lanes 4-7 and 12-15 (banks 1, 3) read lane - 4 (row_ror:4)
-        const int t = __builtin_amdgcn_update_dpp(iv, iv, 0x12C, 0xF, 0x5, false);
-        return __int_as_float(__builtin_amdgcn_update_dpp(t, iv, 0x124, 0xF, 0xA, false));
-    } else {
-        static_assert(S == 8, "dpp_xor: S in 1, 2, 4, 8");
-        return __int_as_float(__builtin_amdgcn_update_dpp(0, iv, 0x128, 0xF, 0xF, false));  // row_ror:8
-    }
-}
-
 // Workgroup (kb, rb), 4 waves x 8 rows (two passes of 4); lane 16 g + i holds
 // elements 8 i .. 8 i + 7 of row 32 rb + 8 wave + 4 pass + g.  H128 stages 1, 2
 // and 4 are inside the lane, 8 .. 64 pair lanes i ^ 1 .. 8 (DPP); the lane's
@@ -1015,7 +995,7 @@ __device__ __forceinline__ void gemm_rows_out(float (&t)[4][NE], int lane, int r
 template <int K, int CB, int RB>
 __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
     const uint8_t *__restrict__ records, int kbs, int nbs, int mtiles, int splits, const uint16_t *__restrict__ xh16,
-    size_t k, float *__restrict__ partials, void *__restrict__ y, int y_f16,
+    size_t k, uint16_t *__restrict__ partials, void *__restrict__ y, int y_f16,
     size_t y_stride, int rows) {
     constexpr int BM = 32 * RB * kGemmWaves;
     constexpr size_t GB = (size_t)2048 * K + 512;
@@ -1184,19 +1164,27 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
     // epilogue.  acc[rb][cb][e]: row 32 RB wave + 32 rb + (e % 4) + 8 (e / 4) + 4 lh,
     // column 32 cb + l32
     if (splits > 1) {
-        // partials in accumulator layout [tile][split][wave][rb][cb][v][lane] x 16
-        // bytes (v = e / 4), summed by gemm_reduce_kernel
-        constexpr size_t kPerSplit = (size_t)kGemmWaves * RB * 4 * 4 * 64 * 4;  // floats
-        float *dst = partials + ((size_t)tile * splits + s) * kPerSplit + (size_t)wave * RB * 16 * 256 + lane * 4;
+        // fp16 partials in accumulator layout [tile][split][wave][rb][cb][vp][lane]
+        // x 16 bytes: elements 8 vp .. 8 vp + 7 of acc[rb][cb] (rows of v = 2 vp,
+        // 2 vp + 1), summed in fp32 by gemm_reduce_kernel.  fp16 keeps the layer
+        // within its tolerance (rel-L2 2.9e-4 against 2.1e-4 for fp32 partials
+        // with fp16 output, at k = 14336) for half the bytes.
+        constexpr size_t kPerSplit = (size_t)kGemmWaves * RB * 4 * 2 * 64 * 8;  // halves
+        uint16_t *dst = partials + ((size_t)tile * splits + s) * kPerSplit + (size_t)wave * RB * 8 * 512 + lane * 8;
+        auto pk = [](float a, float b) {
+            return (uint32_t)float_to_half_bits(a) | ((uint32_t)float_to_half_bits(b) << 16);
+        };
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
             for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-                for (int v = 0; v < 4; ++v)
-                    __builtin_nontemporal_store(
-                        (f4){acc[rb][cb][4 * v], acc[rb][cb][4 * v + 1], acc[rb][cb][4 * v + 2], acc[rb][cb][4 * v + 3]},
-                        (f4 *)(dst + ((rb * 4 + cb) * 4 + v) * 256));
+                for (int vp = 0; vp < 2; ++vp) {
+                    const f16v &a = acc[rb][cb];
+                    const u4 d = {pk(a[8 * vp], a[8 * vp + 1]), pk(a[8 * vp + 2], a[8 * vp + 3]),
+                                  pk(a[8 * vp + 4], a[8 * vp + 5]), pk(a[8 * vp + 6], a[8 * vp + 7])};
+                    __builtin_nontemporal_store(d, (u4 *)(dst + ((rb * 4 + cb) * 2 + vp) * 512));
+                }
         return;
     }
     const uint16_t *svp = (const uint16_t *)(colgroup + 2048 * K + 256);  // record (nb, 0)
@@ -1212,44 +1200,48 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
 }
 
 // Split-K reduction (split count > 1): one wave per (tile, row block blk =
-// RB wave + rb, v) of the GEMM's accumulator layout; lane l sums its 4 x 16
-// bytes of every split in split order (so the result does not depend on the
-// order the GEMM's workgroups ran in), then H128, 1/sqrt(128) and sv over its
-// 8 rows.
+// RB wave + rb, vp) of the GEMM's partial layout; lane l sums its 4 x 16 bytes
+// (fp16) of every split in fp32 in split order (so the result does not depend on
+// the order the GEMM's workgroups ran in), then H128, 1/sqrt(128) and sv over its
+// 16 rows.
 template <int RB>
-__global__ __launch_bounds__(256) void gemm_reduce_kernel(const float *__restrict__ partials, int splits, int nbs,
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(const uint16_t *__restrict__ partials, int splits, int nbs,
                                                           const uint8_t *__restrict__ records, int bits, int kbs,
                                                           void *__restrict__ y, int y_f16, size_t y_stride, int rows,
                                                           int nwaves) {
     constexpr int BM = 32 * RB * kGemmWaves;
-    constexpr size_t kPerSplit = (size_t)kGemmWaves * RB * 4 * 4 * 64 * 4;  // floats
+    constexpr size_t kPerSplit = (size_t)kGemmWaves * RB * 4 * 2 * 64 * 8;  // halves
     const int lane = threadIdx.x & 63;
     const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (gw >= nwaves) return;
-    const int v = gw & 3, blk = (gw >> 2) % (kGemmWaves * RB), tile = (gw >> 2) / (kGemmWaves * RB);
+    const int vp = gw & 1, blk = (gw >> 1) % (kGemmWaves * RB), tile = (gw >> 1) / (kGemmWaves * RB);
     const int mt = tile / nbs, nb = tile - mt * nbs;
-    const float *src = partials + (size_t)tile * splits * kPerSplit + (size_t)blk * 16 * 256 + v * 256 + lane * 4;
-    float t[4][4];
+    const uint16_t *src = partials + (size_t)tile * splits * kPerSplit + (size_t)blk * 8 * 512 + vp * 512 + lane * 8;
+    float t[4][8];
 #pragma unroll 1
     for (int sp0 = 0; sp0 < splits; sp0 += 4) {  // loads of four splits in flight, then their sum in order
-        f4 in[4][4];
+        u4 in[4][4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int sp = sp0 + u < splits ? sp0 + u : splits - 1;
 #pragma unroll
-            for (int cb = 0; cb < 4; ++cb) in[u][cb] = *(const f4 *)(src + (size_t)sp * kPerSplit + cb * 4 * 256);
+            for (int cb = 0; cb < 4; ++cb) in[u][cb] = *(const u4 *)(src + (size_t)sp * kPerSplit + cb * 2 * 512);
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u)
             if (sp0 + u < splits)
 #pragma unroll
-                for (int cb = 0; cb < 4; ++cb)
+                for (int cb = 0; cb < 4; ++cb) {
+                    const uint32_t w[4] = {in[u][cb].x, in[u][cb].y, in[u][cb].z, in[u][cb].w};
 #pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        t[cb][q] = sp0 + u == 0 ? in[u][cb][q] : t[cb][q] + in[u][cb][q];
+                    for (int q = 0; q < 8; ++q) {
+                        const float v = half_bits_to_float((uint16_t)(w[q >> 1] >> (16 * (q & 1))));
+                        t[cb][q] = sp0 + u == 0 ? v : t[cb][q] + v;
+                    }
+                }
     }
     const uint16_t *svp = (const uint16_t *)(records + (size_t)nb * kbs * group_bytes(bits) + 2048 * bits + 256);
-    gemm_rows_out<4>(t, lane, mt * BM + 32 * blk + 8 * v, svp, rows, y, y_f16, y_stride, (size_t)nb * 128);
+    gemm_rows_out<8>(t, lane, mt * BM + 32 * blk + 16 * vp, svp, rows, y, y_f16, y_stride, (size_t)nb * 128);
 }
 
 int gemm_tile_rows(size_t rows) { return rows <= 128 ? 128 : 256; }
@@ -1273,7 +1265,7 @@ GemmPlan gemm_plan(size_t k, size_t n, size_t rows) {
     p.xh_off = off;
     off += ((size_t)p.mtiles * p.bm * k * 2 + 255) & ~(size_t)255;
     p.partials_off = off;
-    if (s > 1) off += (size_t)tiles * s * p.bm * 128 * 4;
+    if (s > 1) off += (size_t)tiles * s * p.bm * 128 * 2;  // fp16 partials
     p.bytes = (off + 255) & ~(size_t)255;
     return p;
 }
@@ -1282,8 +1274,8 @@ template <int K, int CB>
 static void launch_gemm_kc(const uint8_t *rec, size_t k, uint16_t *xh, size_t rows, void *y, int y_f16,
                            size_t y_stride, uint8_t *ws, const GemmPlan &p, hipStream_t stream) {
     const dim3 grid((unsigned)(p.mtiles * p.nbs * p.splits)), block(kGemmWaves * 64);
-    float *part = (float *)(ws + p.partials_off);
-    const int nwaves = p.mtiles * p.nbs * (p.bm / 8);  // reduction: one wave per 8 rows of a tile
+    uint16_t *part = (uint16_t *)(ws + p.partials_off);
+    const int nwaves = p.mtiles * p.nbs * (p.bm / 16);  // reduction: one wave per 16 rows of a tile
     const dim3 rgrid((unsigned)((nwaves + 3) / 4));
     if (p.bm == 128) {
         gemm_kernel<K, CB, 1><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, xh, k, part, y, y_f16,
