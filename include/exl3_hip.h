@@ -99,6 +99,27 @@ exl3_status exl3_hip_mul_mat(const void *records, unsigned bits, unsigned codebo
                              void *y, exl3_dtype yt, size_t y_row_stride,
                              void *workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* One matrix of an exl3_hip_mul_mat_group call. */
+typedef struct exl3_matrix_desc {
+    const void *records;   /* device, (n/128)*(k/128) group records, 16-byte aligned */
+    size_t n;              /* output features, multiple of 128 */
+    void *y;               /* device, rows x n of the call's yt */
+    size_t y_row_stride;   /* elements, >= n */
+} exl3_matrix_desc;
+
+/* y_i = layer_i(x) for 1..4 matrices that share k, bits, codebook, x and rows
+ * (the q/k/v or gate/up projections of one decoder layer): at rows <=
+ * exl3_hip_gemv_max_rows() one GEMV launch serves all of them, so the launch and
+ * its latency chain are paid once; larger row counts run one exl3_hip_mul_mat
+ * per matrix.  Each y_i is the exl3_hip_mul_mat result within the layer
+ * tolerance (the split of k follows the total width, so the summation order may
+ * differ from a single call's).  workspace: >= exl3_hip_mul_mat_workspace_bytes(k,
+ * sum of n_i, rows), or NULL for the internal one.  This entry point has no
+ * counterpart in the reference, whose ggml op multiplies one matrix per call. */
+exl3_status exl3_hip_mul_mat_group(const exl3_matrix_desc *mats, size_t count, unsigned bits, unsigned codebook,
+                                   size_t k, const void *x, exl3_dtype xt, size_t rows, size_t x_row_stride,
+                                   exl3_dtype yt, void *workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* Decode packed weights to row-major fp16 bits out[k][column_count] for
  * columns [first_column, first_column + column_count), bit-exact with
  * exl3::decode_inner_slice.  UPSTREAM_TILES: k, n, first and count multiples

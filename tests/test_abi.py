@@ -59,6 +59,15 @@ def test_host_side_status_and_planning():
     assert L.exl3_hip_mul_mat(None, 4, 2, 128, 128, None, 1, 1, 128, None, 0, 128, None, 0, None) == 1
     assert L.exl3_hip_decode(None, 0, 4, 2, 16, 16, 0, 16, None, None) == 1
     assert L.exl3_hip_get_rows(None, 4, 2, 128, 128, None, 1, None, 0, 128, None, None) == 1
+    assert L.exl3_hip_mul_mat_group(None, 1, 4, 2, 2048, None, 1, 1, 2048, 1, None, 0, None) == 1
+    import ctypes
+    descs = (ctypes.c_size_t * 4)(0, 128, 0, 128)   # one descriptor: NULL records
+    assert L.exl3_hip_mul_mat_group(ctypes.cast(descs, ctypes.c_void_p), 0, 4, 2, 128, None, 1, 1, 128, 1,
+                                    None, 0, None) == 1   # count 0
+    assert L.exl3_hip_mul_mat_group(ctypes.cast(descs, ctypes.c_void_p), 5, 4, 2, 128, None, 1, 1, 128, 1,
+                                    None, 0, None) == 1   # more than 4 matrices
+    assert L.exl3_hip_mul_mat_group(ctypes.cast(descs, ctypes.c_void_p), 1, 4, 2, 128, None, 1, 1, 128, 1,
+                                    None, 0, None) == 1   # NULL records
     assert L.exl3_hip_get_rows(None, 4, 2, 100, 128, None, 1, None, 0, 128, None, None) == 1
     assert L.exl3_hip_get_rows(None, 4, 2, 128, 128, None, 0, None, 0, 128, None, None) == 0  # count 0: no-op
     assert L.exl3_hip_hadamard128(None, 100, None) == 1

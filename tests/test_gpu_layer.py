@@ -228,3 +228,24 @@ def test_one_workspace_serves_mixed_row_counts(amd):
         torch.cuda.synchronize()
         assert torch.equal(y_shared, fresh[r]), f"caller workspace, call {i} rows={r}"
         assert torch.equal(y_internal, fresh[r]), f"internal workspace, call {i} rows={r}"
+
+
+@pytest.mark.parametrize("rows", [1, 3, 8, 12])
+def test_group_matches_single_layers(amd, oracle, rows):
+    """q/k/v and gate/up of one decoder layer through exl3_hip_mul_mat_group: one launch
+    (rows <= 8) that serves several matrices sharing x; each output within the layer
+    tolerance of the oracle, and at rows > 8 (one call per matrix) equal to mul_mat"""
+    import torch
+    for k, shapes, bits in [(2048, [2048, 512, 512], 6), (2048, [6144, 6144], 4)]:
+        recs = [make_layer(700 + i + bits, k, n, bits) for i, n in enumerate(shapes)]
+        x = synth.activations(800 + rows, rows, k)
+        xd = torch.from_numpy(x).cuda()
+        ys = amd.mul_mat_group([(dev(r), n) for r, n in zip(recs, shapes)], bits, k, xd)
+        for i, (r, n) in enumerate(zip(recs, shapes)):
+            y = ys[i].cpu().numpy()
+            assert_layer_close(y, oracle.mul_mat(r, bits, 2, k, n, x), what=f"group {i} n={n} rows={rows}")
+            if rows > 8:
+                single = amd.mul_mat(dev(r), bits, k, n, xd).cpu().numpy()
+                assert np.array_equal(y, single)
+    L = amd.lib()
+    assert L.exl3_hip_mul_mat_group(None, 1, 4, 2, 2048, None, 1, 1, 2048, 1, None, 0, None) == 1

@@ -138,6 +138,50 @@ exl3_status exl3_hip_mul_mat(const void *records, unsigned bits, unsigned codebo
                                        y_row_stride, workspace, exl3k::gemm_plan(k, n, rows), stream));
 }
 
+exl3_status exl3_hip_mul_mat_group(const exl3_matrix_desc *mats, size_t count, unsigned bits, unsigned codebook,
+                                   size_t k, const void *x, exl3_dtype xt, size_t rows, size_t x_row_stride,
+                                   exl3_dtype yt, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (!mats || count < 1 || count > (size_t)exl3k::kGemvMaxTargets) return EXL3_INVAL_PARAMS;
+    size_t n_total = 0;
+    for (size_t i = 0; i < count; ++i) {
+        const exl3_matrix_desc &m = mats[i];
+        if (!exl3_hip_supports_mul_mat(bits, codebook, k, m.n, rows, xt, yt)) return EXL3_INVAL_PARAMS;
+        if (!m.records || !m.y || !aligned(m.records, 16) || !aligned(m.y, dtype_size(yt)) || m.y_row_stride < m.n)
+            return EXL3_INVAL_PARAMS;
+        n_total += m.n;
+    }
+    if (!x || !aligned(x, dtype_size(xt)) || x_row_stride < k || n_total > kMaxDim) return EXL3_INVAL_PARAMS;
+    if (rows > (size_t)exl3k::kGemvMaxRows) {  // GEMM row counts: one call per matrix, each a full-size launch
+        for (size_t i = 0; i < count; ++i) {
+            const exl3_status st = exl3_hip_mul_mat(mats[i].records, bits, codebook, k, mats[i].n, x, xt, rows,
+                                                    x_row_stride, mats[i].y, yt, mats[i].y_row_stride, workspace,
+                                                    workspace_bytes, stream);
+            if (st != EXL3_OK) return st;
+        }
+        return EXL3_OK;
+    }
+    const size_t need = exl3_hip_mul_mat_workspace_bytes(k, n_total, rows);
+    if (workspace) {
+        if (!aligned(workspace, 256)) return EXL3_INVAL_PARAMS;
+        if (workspace_bytes < need) return EXL3_WORKSPACE_TOO_SMALL;
+    } else {
+        const exl3_status st = internal_workspace(need, n_total, stream, &workspace);
+        if (st != EXL3_OK) return st;
+    }
+    exl3k::GemvTargets tg{};
+    int nb_end = 0;
+    for (size_t i = 0; i < count; ++i) {
+        tg.records[i] = (const uint8_t *)mats[i].records;
+        tg.y[i] = mats[i].y;
+        tg.y_stride[i] = mats[i].y_row_stride;
+        nb_end += (int)(mats[i].n / 128);
+        tg.nb_end[i] = nb_end;
+    }
+    tg.count = (int)count;
+    return from_hip(exl3k::launch_gemv_targets(tg, (int)bits, (int)codebook, x, xt == EXL3_F16, rows, x_row_stride,
+                                               yt == EXL3_F16, workspace, exl3k::gemv_plan(k, n_total, rows), stream));
+}
+
 exl3_status exl3_hip_decode(const void *src, exl3_layout layout, unsigned bits, unsigned codebook, size_t k, size_t n,
                             size_t first_column, size_t column_count, uint16_t *out, hipStream_t stream) {
     if (!valid_rate(bits, codebook) || !src || !out || !aligned(src, 16) || !aligned(out, 16)) return EXL3_INVAL_PARAMS;

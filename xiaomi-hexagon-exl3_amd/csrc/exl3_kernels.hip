@@ -550,9 +550,8 @@ __device__ __forceinline__ void load_chunk(const uint8_t *p, uint32_t (&w)[K]) {
 
 template <int K, int CB>
 __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
-    const uint8_t *__restrict__ records, int kbs, int nbs, int splits, const void *__restrict__ x, int x_f16,
-    size_t x_stride, int rows, const uint8_t *__restrict__ dummy, float *__restrict__ partials,
-    unsigned *__restrict__ counters, void *__restrict__ y, int y_f16, size_t y_stride) {
+    GemvTargets tg, int kbs, int nbs, int splits, const void *__restrict__ x, int x_f16, size_t x_stride, int rows,
+    const uint8_t *__restrict__ dummy, float *__restrict__ partials, unsigned *__restrict__ counters, int y_f16) {
     constexpr int W = kGemvWaves;
     constexpr int P = W / 4;  // waves per column pair
     constexpr int NT = W * 64;
@@ -569,7 +568,24 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
     const int s = blockIdx.x / nbs, nb = blockIdx.x - s * nbs;
     const int kb0 = (int)((long long)kbs * s / splits), kb1 = (int)((long long)kbs * (s + 1) / splits);
     const int nkb = kb1 - kb0;
-    const uint8_t *colgroup = records + (size_t)nb * kbs * GB;
+    // the matrix of column group nb (targets share k, x and the bit rate)
+    int mi = 0;
+#pragma unroll
+    for (int i = 1; i < kGemvMaxTargets; ++i)
+        if (i < tg.count && nb >= tg.nb_end[i - 1]) mi = i;
+    const uint8_t *records = tg.records[0];
+    void *y = tg.y[0];
+    size_t y_stride = tg.y_stride[0];
+    int nbl = nb;  // column group within the matrix
+#pragma unroll
+    for (int i = 1; i < kGemvMaxTargets; ++i)
+        if (mi == i) {
+            records = tg.records[i];
+            y = tg.y[i];
+            y_stride = tg.y_stride[i];
+            nbl = nb - tg.nb_end[i - 1];
+        }
+    const uint8_t *colgroup = records + (size_t)nbl * kbs * GB;
 
     // 1. activations: all loads first, then the conversions (which wait for them)
     const int nblk = nkb * rows;
@@ -744,7 +760,7 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
         h128_wave(a0, a1, lane);
         a0 *= sv0;
         a1 *= sv1;
-        const size_t o = (size_t)rr * y_stride + (size_t)nb * 128;
+        const size_t o = (size_t)rr * y_stride + (size_t)nbl * 128;
         if (y_f16) {
             ((uint16_t *)y)[o + lane] = float_to_half_bits(a0);
             ((uint16_t *)y)[o + lane + 64] = float_to_half_bits(a1);
@@ -792,25 +808,38 @@ GemvPlan gemv_plan(size_t k, size_t n, size_t rows) {
 }
 
 template <int K, int CB>
-static hipError_t launch_gemv_kc(const uint8_t *rec, const void *x, int x_f16, size_t rows, size_t x_stride, void *y,
-                                 int y_f16, size_t y_stride, uint8_t *ws, const GemvPlan &p, hipStream_t stream) {
+static hipError_t launch_gemv_kc(const GemvTargets &tg, const void *x, int x_f16, size_t rows, size_t x_stride,
+                                 int y_f16, uint8_t *ws, const GemvPlan &p, hipStream_t stream) {
     const size_t lds = gemv_lds_bytes(p.nkw, rows);
     const dim3 grid((unsigned)(p.nbs * p.splits)), block(kGemvWaves * 64);
-    gemv_kernel<K, CB><<<grid, block, lds, stream>>>(rec, p.kbs, p.nbs, p.splits, x, x_f16, x_stride, (int)rows,
+    gemv_kernel<K, CB><<<grid, block, lds, stream>>>(tg, p.kbs, p.nbs, p.splits, x, x_f16, x_stride, (int)rows,
                                                      ws + p.dummy_off, (float *)(ws + p.partials_off),
-                                                     (unsigned *)(ws + p.counters_off), y, y_f16, y_stride);
+                                                     (unsigned *)(ws + p.counters_off), y_f16);
     return hipGetLastError();
 }
 
 template <int K>
-static hipError_t launch_gemv_k(const void *records, int cb, const void *x, int x_f16, size_t rows, size_t x_stride,
-                                void *y, int y_f16, size_t y_stride, uint8_t *ws, const GemvPlan &p,
-                                hipStream_t stream) {
-    const uint8_t *rec = (const uint8_t *)records;
+static hipError_t launch_gemv_k(const GemvTargets &tg, int cb, const void *x, int x_f16, size_t rows, size_t x_stride,
+                                int y_f16, uint8_t *ws, const GemvPlan &p, hipStream_t stream) {
     switch (cb) {
-    case 0: return launch_gemv_kc<K, 0>(rec, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
-    case 1: return launch_gemv_kc<K, 1>(rec, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
-    default: return launch_gemv_kc<K, 2>(rec, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
+    case 0: return launch_gemv_kc<K, 0>(tg, x, x_f16, rows, x_stride, y_f16, ws, p, stream);
+    case 1: return launch_gemv_kc<K, 1>(tg, x, x_f16, rows, x_stride, y_f16, ws, p, stream);
+    default: return launch_gemv_kc<K, 2>(tg, x, x_f16, rows, x_stride, y_f16, ws, p, stream);
+    }
+}
+
+hipError_t launch_gemv_targets(const GemvTargets &tg, int bits, int cb, const void *x, int x_f16, size_t rows,
+                               size_t x_stride, int y_f16, void *workspace, const GemvPlan &p, hipStream_t stream) {
+    uint8_t *ws = (uint8_t *)workspace;
+    switch (bits) {
+    case 1: return launch_gemv_k<1>(tg, cb, x, x_f16, rows, x_stride, y_f16, ws, p, stream);
+    case 2: return launch_gemv_k<2>(tg, cb, x, x_f16, rows, x_stride, y_f16, ws, p, stream);
+    case 3: return launch_gemv_k<3>(tg, cb, x, x_f16, rows, x_stride, y_f16, ws, p, stream);
+    case 4: return launch_gemv_k<4>(tg, cb, x, x_f16, rows, x_stride, y_f16, ws, p, stream);
+    case 5: return launch_gemv_k<5>(tg, cb, x, x_f16, rows, x_stride, y_f16, ws, p, stream);
+    case 6: return launch_gemv_k<6>(tg, cb, x, x_f16, rows, x_stride, y_f16, ws, p, stream);
+    case 7: return launch_gemv_k<7>(tg, cb, x, x_f16, rows, x_stride, y_f16, ws, p, stream);
+    default: return launch_gemv_k<8>(tg, cb, x, x_f16, rows, x_stride, y_f16, ws, p, stream);
     }
 }
 
@@ -818,18 +847,13 @@ hipError_t launch_gemv(const void *records, int bits, int cb, size_t k, size_t n
                        size_t rows, size_t x_stride, void *y, int y_f16, size_t y_stride, void *workspace,
                        const GemvPlan &p, hipStream_t stream) {
     (void)k;
-    (void)n;
-    uint8_t *ws = (uint8_t *)workspace;
-    switch (bits) {
-    case 1: return launch_gemv_k<1>(records, cb, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
-    case 2: return launch_gemv_k<2>(records, cb, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
-    case 3: return launch_gemv_k<3>(records, cb, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
-    case 4: return launch_gemv_k<4>(records, cb, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
-    case 5: return launch_gemv_k<5>(records, cb, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
-    case 6: return launch_gemv_k<6>(records, cb, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
-    case 7: return launch_gemv_k<7>(records, cb, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
-    default: return launch_gemv_k<8>(records, cb, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
-    }
+    GemvTargets tg{};
+    tg.records[0] = (const uint8_t *)records;
+    tg.y[0] = y;
+    tg.y_stride[0] = y_stride;
+    tg.nb_end[0] = (int)(n / 128);
+    tg.count = 1;
+    return launch_gemv_targets(tg, bits, cb, x, x_f16, rows, x_stride, y_f16, workspace, p, stream);
 }
 
 // ============================================================== GEMM

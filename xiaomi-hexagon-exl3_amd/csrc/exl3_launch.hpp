@@ -22,6 +22,18 @@ constexpr int kGemmWaves = 4;
 constexpr size_t kGemmSplitTiles = 512;
 inline size_t counter_region_bytes(size_t n) { return (n / 128 * 4 + 255) & ~(size_t)255; }
 
+// Up to kGemvMaxTargets matrices that share k, the bit rate, the codebook and x,
+// served by one GEMV launch: column groups [nb_end[i-1], nb_end[i]) belong to
+// matrix i (records[i], output y[i] with row stride y_stride[i] elements).
+constexpr int kGemvMaxTargets = 4;
+struct GemvTargets {
+    const uint8_t *records[kGemvMaxTargets];
+    void *y[kGemvMaxTargets];
+    size_t y_stride[kGemvMaxTargets];
+    int nb_end[kGemvMaxTargets];
+    int count;
+};
+
 struct GemvPlan {
     int nbs, kbs, splits, nkw;  // nkw: largest kb count of a split
     size_t counters_off, dummy_off, partials_off, bytes;
@@ -38,6 +50,8 @@ int gemm_tile_rows(size_t rows);
 hipError_t launch_gemv(const void *records, int bits, int cb, size_t k, size_t n, const void *x, int x_f16,
                        size_t rows, size_t x_stride, void *y, int y_f16, size_t y_stride, void *workspace,
                        const GemvPlan &plan, hipStream_t stream);
+hipError_t launch_gemv_targets(const GemvTargets &targets, int bits, int cb, const void *x, int x_f16, size_t rows,
+                               size_t x_stride, int y_f16, void *workspace, const GemvPlan &plan, hipStream_t stream);
 hipError_t launch_gemm(const void *records, int bits, int cb, size_t k, size_t n, const void *x, int x_f16,
                        size_t rows, size_t x_stride, void *y, int y_f16, size_t y_stride, void *workspace,
                        const GemmPlan &plan, hipStream_t stream);

@@ -20,6 +20,7 @@ EXPORTS = [
     "exl3_hip_mul_mat_workspace_bytes", "exl3_hip_workspace_init", "exl3_hip_mul_mat", "exl3_hip_decode",
     "exl3_hip_reconstruct", "exl3_hip_get_rows", "exl3_hip_codebook", "exl3_hip_hadamard128",
     "exl3_hip_pack_records", "exl3_hip_validate_records",
+    "exl3_hip_mul_mat_group",
     "exl3_hip_model_open", "exl3_hip_model_close", "exl3_hip_model_tensor_count", "exl3_hip_model_payload_bytes",
     "exl3_hip_model_hidden_size", "exl3_hip_model_vocab_size", "exl3_hip_model_bits_per_weight",
     "exl3_hip_model_embedding", "exl3_hip_model_matrix_count", "exl3_hip_model_matrix", "exl3_hip_model_record_bytes",
@@ -52,6 +53,8 @@ def load(path=LIB_PATH):
     L.exl3_hip_workspace_init.argtypes = [vp, sz, st]
     L.exl3_hip_mul_mat.restype = i
     L.exl3_hip_mul_mat.argtypes = [vp, u, u, sz, sz, vp, i, sz, sz, vp, i, sz, vp, sz, st]
+    L.exl3_hip_mul_mat_group.restype = i
+    L.exl3_hip_mul_mat_group.argtypes = [vp, sz, u, u, sz, vp, i, sz, sz, i, vp, sz, st]
     L.exl3_hip_decode.restype = i
     L.exl3_hip_decode.argtypes = [vp, i, u, u, sz, sz, sz, sz, vp, st]
     L.exl3_hip_reconstruct.restype = i
@@ -138,6 +141,33 @@ def mul_mat(records, bits, k, n, x, codebook=CB_MUL1, out_dtype=None, y=None, wo
     _check(lib().exl3_hip_mul_mat(_ptr(records), bits, codebook, k, n, _ptr(x), xt, rows, x.stride(0), _ptr(y), yt,
                                   y.stride(0), ws_ptr, ws_bytes, _stream(stream)), "mul_mat")
     return y
+
+
+class _MatrixDesc(ctypes.Structure):
+    _fields_ = [("records", ctypes.c_void_p), ("n", ctypes.c_size_t), ("y", ctypes.c_void_p),
+                ("y_row_stride", ctypes.c_size_t)]
+
+
+def mul_mat_group(mats, bits, k, x, codebook=CB_MUL1, out_dtype=None, workspace=None, stream=None):
+    """[y_i] = layer_i(x) for matrices [(records_i, n_i)] (or (records_i, n_i, y_i)) sharing k, bits, codebook
+    and x: one launch at rows <= 8."""
+    import torch
+    assert x.dim() == 2 and x.stride(1) == 1 and x.dtype in (torch.float16, torch.float32)
+    rows = x.shape[0]
+    ys, descs = [], (_MatrixDesc * len(mats))()
+    for idx, m in enumerate(mats):
+        rec, n = m[0], m[1]
+        y = m[2] if len(m) > 2 else torch.empty((rows, n), dtype=out_dtype or torch.float32, device=x.device)
+        assert y.dim() == 2 and y.stride(1) == 1
+        descs[idx] = _MatrixDesc(rec.data_ptr(), n, y.data_ptr(), y.stride(0))
+        ys.append(y)
+    yt = F16 if ys[0].dtype == torch.float16 else F32
+    assert all(y.dtype == ys[0].dtype for y in ys)
+    xt = F16 if x.dtype == torch.float16 else F32
+    ws_ptr, ws_bytes = (None, 0) if workspace is None else (_ptr(workspace), workspace.numel())
+    _check(lib().exl3_hip_mul_mat_group(ctypes.cast(descs, ctypes.c_void_p), len(mats), bits, codebook, k, _ptr(x), xt,
+                                        rows, x.stride(0), yt, ws_ptr, ws_bytes, _stream(stream)), "mul_mat_group")
+    return ys
 
 
 def decode(src, bits, k, n, codebook=CB_MUL1, layout=LAYOUT_UPSTREAM_TILES, first=0, count=None, out=None,
