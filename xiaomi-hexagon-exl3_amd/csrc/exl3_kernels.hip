@@ -498,12 +498,13 @@ __device__ __forceinline__ float load_x(const void *x, int x_f16, size_t stride,
 //      src/exl3-ggml.cpp:60-73) for every (kb, r) of the workgroup, split into
 //      fp16 hi = rn(xh) and lo = rn(xh - hi) and stored in LDS as MFMA B
 //      fragments: column m < 8 carries hi of row m, column m >= 8 lo of row m - 8.
-//      The activation loads are issued first, so they return first.
+//      All activation loads of a wave are in flight together.
 //   2. weight stream: lane l = 16 g + i loads chunk i % 8 (K contiguous words)
 //      of tile (4 r4 + g, 2 c2 + i / 8): one K-word load per lane and group,
-//      DEPTH groups in flight; EARLY of them before the prep barrier, the rest
-//      after it, so that no wave reaches the barrier late because the chip's
-//      memory pipeline refuses its loads.
+//      DEPTH groups in flight, all issued after the prep barrier: weight loads
+//      issued earlier delay the activation loads of the other workgroups behind
+//      them (measured: 3 groups before the barrier cost 4 % at k = 14336, all 8
+//      cost 11 %), and the prep is on every workgroup's critical path.
 //   3. a lane decodes its chunk's 32 weights in registers (the first states
 //      reach into the previous chunk's last word, taken from the neighbouring
 //      lane with DPP) into four MFMA A fragments (rows 0-7 / 8-15 of its tile row
@@ -517,7 +518,6 @@ __device__ __forceinline__ float load_x(const void *x, int x_f16, size_t stride,
 template <int K>
 struct GemvStream {
     static constexpr int DEPTH = K <= 2 ? 12 : (K <= 4 ? 8 : 4);  // groups in flight per wave
-    static constexpr int EARLY = DEPTH < 3 ? DEPTH : 3;           // of them issued before the prep barrier
 };
 constexpr int kGemvPrepMax = 16;          // (kb, row) prep blocks per wave
 constexpr size_t kGemvDummyBytes = 8192;  // >= largest lane offset of a group + its K words (1024 K)
@@ -587,46 +587,10 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
         }
     const uint8_t *colgroup = records + (size_t)nbl * kbs * GB;
 
-    // 1. activations: all loads first, then the conversions (which wait for them)
-    const int nblk = nkb * rows;
-    float pv0[kGemvPrepMax], pv1[kGemvPrepMax];
-    auto prep_inputs = [&](auto is_f16) {
-        constexpr bool XF16 = decltype(is_f16)::value;
-        uint32_t px0[kGemvPrepMax], px1[kGemvPrepMax], ps[kGemvPrepMax];
-#pragma unroll
-        for (int q = 0; q < kGemvPrepMax; ++q) {
-            const int blk = wave + q * W;
-            if (blk < nblk) {
-                const int kbl = blk / rows, r = blk - kbl * rows;
-                const int kb = kb0 + kbl;
-                ps[q] = ((const uint32_t *)(records + (size_t)kb * GB + 2048 * K))[lane];  // record (0, kb): su pair
-                const size_t xi = (size_t)r * x_stride + (size_t)kb * 128 + 2 * lane;
-                if constexpr (XF16) {
-                    px0[q] = ((const uint16_t *)x)[xi];
-                    px1[q] = ((const uint16_t *)x)[xi + 1];
-                } else {
-                    px0[q] = ((const uint32_t *)x)[xi];
-                    px1[q] = ((const uint32_t *)x)[xi + 1];
-                }
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < kGemvPrepMax; ++q) {
-            if (wave + q * W < nblk) {
-                const float x0 = XF16 ? half_bits_to_float((uint16_t)px0[q]) : bitcast<float>(px0[q]);
-                const float x1 = XF16 ? half_bits_to_float((uint16_t)px1[q]) : bitcast<float>(px1[q]);
-                pv0[q] = x0 * half_bits_to_float((uint16_t)(ps[q] & 0xffffu));
-                pv1[q] = x1 * half_bits_to_float((uint16_t)(ps[q] >> 16));
-            }
-        }
-    };
-    if (x_f16) prep_inputs(std::true_type{});
-    else prep_inputs(std::false_type{});
     // output scales for the epilogue (record (nb, 0), src/exl3-ggml.cpp:84-85)
     const uint16_t *svp = (const uint16_t *)(colgroup + 2048 * K + 256);
-    const float sv0 = half_bits_to_float(svp[lane]), sv1 = half_bits_to_float(svp[lane + 64]);
 
-    // 2. weight stream: this wave's groups are q = part + P i; issues past its
+    // weight stream: this wave's groups are q = part + P i; issues past its
     // last group read the workspace's dummy region, so every issue is
     // unconditional and the compiler's wait counts stay exact
     const int g = lane >> 4, li = lane & 15, j = li & 7;
@@ -639,21 +603,47 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
                            : dummy + lane_off;
     };
     uint32_t buf[D][K];
-#pragma unroll
-    for (int d = 0; d < GemvStream<K>::EARLY; ++d) load_chunk<K>(group_src(d), buf[d]);
 
-    // 3. prep arithmetic under the stream's first latency: H128 per (kb, row),
-    // hi/lo fp16 pairs into the fragment blocks.  Element 2 lane (+1) of block kb
-    // is tile row lane / 8 (r4 = lane / 32, kg = lane / 8 % 4), rows
-    // 2 (lane % 8) (+1): half (lane / 4) % 2, fragment elements 2 (lane % 4) (+1).
-    {
+    // 1. loads: the activation pair and su pair of each of this wave's (kb, row)
+    // prep blocks blk = wave + W q.  NQ (slots per wave) is a compile-time bound
+    // and a slot past the last block re-reads that block (never used), so the
+    // loads are straight-line code and all in flight together: with a branch per
+    // slot the compiler pulls each conversion up to its load and waits there,
+    // one round trip per slot.
+    // 2. prep arithmetic: x su, H128 per (kb, row), hi/lo fp16 pairs into the
+    // fragment blocks.  Element 2 lane (+1) of block kb is tile row lane / 8 (r4 = lane / 32,
+    // kg = lane / 8 % 4), rows 2 (lane % 8) (+1): half (lane / 4) % 2, fragment
+    // elements 2 (lane % 4) (+1).
+    const int nblk = nkb * rows;
+    auto prologue = [&](auto nq_c, auto is_f16) {
+        constexpr int NQ = decltype(nq_c)::value;
+        constexpr bool XF16 = decltype(is_f16)::value;
+        uint32_t px0[NQ], px1[NQ], ps[NQ];
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            const int blk = wave + q * W < nblk ? wave + q * W : nblk - 1;
+            const int kbl = blk / rows, r = blk - kbl * rows;
+            const int kb = kb0 + kbl;
+            ps[q] = ((const uint32_t *)(records + (size_t)kb * GB + 2048 * K))[lane];  // record (0, kb): su pair
+            const size_t xi = (size_t)r * x_stride + (size_t)kb * 128 + 2 * lane;
+            if constexpr (XF16) {
+                px0[q] = ((const uint16_t *)x)[xi];
+                px1[q] = ((const uint16_t *)x)[xi + 1];
+            } else {
+                px0[q] = ((const uint32_t *)x)[xi];
+                px1[q] = ((const uint32_t *)x)[xi + 1];
+            }
+        }
         const int r4 = lane >> 5, kg = (lane >> 3) & 3, half = (lane >> 2) & 1, jj = 2 * (lane & 3);
 #pragma unroll
-        for (int q = 0; q < kGemvPrepMax; ++q) {
+        for (int q = 0; q < NQ; ++q) {
             const int blk = wave + q * W;
             if (blk < nblk) {
                 const int kbl = blk / rows, r = blk - kbl * rows;
-                float a = pv0[q], b = pv1[q];
+                const float x0 = XF16 ? half_bits_to_float((uint16_t)px0[q]) : bitcast<float>(px0[q]);
+                const float x1 = XF16 ? half_bits_to_float((uint16_t)px1[q]) : bitcast<float>(px1[q]);
+                float a = x0 * half_bits_to_float((uint16_t)(ps[q] & 0xffffu));
+                float b = x1 * half_bits_to_float((uint16_t)(ps[q] >> 16));
                 h128_pair(a, b, lane);
                 const _Float16 ha = (_Float16)a, hb = (_Float16)b;
                 const h2 hi = {ha, hb}, lo = {(_Float16)(a - (float)ha), (_Float16)(b - (float)hb)};
@@ -662,10 +652,21 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
                 *(h2 *)(bp + ((kg * 2 + 1) * rows + r) * 16) = lo;
             }
         }
-    }
+    };
+    auto prologue_x = [&](auto is_f16) {
+        const int nq = (nblk + W - 1) / W;  // slots of wave 0 (the most)
+        if (nq <= 1) prologue(std::integral_constant<int, 1>{}, is_f16);
+        else if (nq <= 2) prologue(std::integral_constant<int, 2>{}, is_f16);
+        else if (nq <= 4) prologue(std::integral_constant<int, 4>{}, is_f16);
+        else if (nq <= 8) prologue(std::integral_constant<int, 8>{}, is_f16);
+        else prologue(std::integral_constant<int, kGemvPrepMax>{}, is_f16);
+    };
+    if (x_f16) prologue_x(std::true_type{});
+    else prologue_x(std::false_type{});
+    const float sv0 = half_bits_to_float(svp[lane]), sv1 = half_bits_to_float(svp[lane + 64]);
     __syncthreads();
 #pragma unroll
-    for (int d = GemvStream<K>::EARLY; d < D; ++d) load_chunk<K>(group_src(d), buf[d]);
+    for (int d = 0; d < D; ++d) load_chunk<K>(group_src(d), buf[d]);
 
     // 4. decode + MFMA.  B operand lane l: m = l % 16 -> (hl, row) = (m / 8, m % 8),
     // k group l / 16; rows >= `rows` read the last row (their columns are discarded)
