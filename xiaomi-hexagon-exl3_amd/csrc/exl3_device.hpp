@@ -193,9 +193,9 @@ template <int S>
 __device__ __forceinline__ float dpp_xor(float v) {
     const int iv = __float_as_int(v);
     if constexpr (S == 1) {
-        return __int_as_float(__builtin_amdgcn_update_dpp(0, iv, 0xB1, 0xF, 0xF, false));  // quad_perm 1,0,3,2
+        return __int_as_float(__builtin_amdgcn_mov_dpp(iv, 0xB1, 0xF, 0xF, false));  // quad_perm 1,0,3,2
     } else if constexpr (S == 2) {
-        return __int_as_float(__builtin_amdgcn_update_dpp(0, iv, 0x4E, 0xF, 0xF, false));  // quad_perm 2,3,0,1
+        return __int_as_float(__builtin_amdgcn_mov_dpp(iv, 0x4E, 0xF, 0xF, false));  // quad_perm 2,3,0,1
     } else if constexpr (S == 4) {
         // lanes 0-3 and 8-11 of the row (banks 0, 2) read lane + 4 (row_ror:12),
         // lanes 4-7 and 12-15 (banks 1, 3) read lane - 4 (row_ror:4)
@@ -203,7 +203,7 @@ __device__ __forceinline__ float dpp_xor(float v) {
         return __int_as_float(__builtin_amdgcn_update_dpp(t, iv, 0x124, 0xF, 0xA, false));
     } else {
         static_assert(S == 8, "dpp_xor: S in 1, 2, 4, 8");
-        return __int_as_float(__builtin_amdgcn_update_dpp(0, iv, 0x128, 0xF, 0xF, false));  // row_ror:8
+        return __int_as_float(__builtin_amdgcn_mov_dpp(iv, 0x128, 0xF, 0xF, false));  // row_ror:8
     }
 }
 

@@ -676,8 +676,8 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
     f4 acc1 = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
     auto mac = [&](int i, const uint32_t (&w)[K]) {
         // last word of the previous chunk of the same tile: lane i - 1, or i + 7 for chunk 0
-        const uint32_t p1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)w[K - 1], 0x121, 0xF, 0xF, false);  // row_ror:1
-        const uint32_t p9 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)w[K - 1], 0x129, 0xF, 0xF, false);  // row_ror:9
+        const uint32_t p1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)w[K - 1], 0x121, 0xF, 0xF, false);  // row_ror:1
+        const uint32_t p9 = (uint32_t)__builtin_amdgcn_mov_dpp((int)w[K - 1], 0x129, 0xF, 0xF, false);  // row_ror:9
         u4 fr[4];
         decode_chunk<K, CB>(w, first_chunk ? p9 : p1, fr);
         const uint8_t *bp = frag + (size_t)group_q(i) * 2 * blk_bytes + boff;
@@ -910,31 +910,49 @@ __global__ __launch_bounds__(256) void gemm_xprep_kernel(const uint8_t *__restri
     }
     if (x_f16) xprep_load<true>(x, off, v);  // all loads before the first use
     else xprep_load<false>(x, off, v);
+    // stage-major over the 16 values of both passes: independent DPP reads and
+    // butterflies back to back, no wait states between a write and its DPP read
 #pragma unroll
     for (int ps = 0; ps < 2; ++ps) {
         const int r = 32 * rb + 8 * wave + 4 * ps + g;
-        float *e = v[ps];
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-            e[j] = r < rows ? e[j] * half_bits_to_float((uint16_t)(suw[j >> 1] >> (16 * (j & 1)))) : 0.f;
+            v[ps][j] = r < rows ? v[ps][j] * half_bits_to_float((uint16_t)(suw[j >> 1] >> (16 * (j & 1)))) : 0.f;
+    }
 #pragma unroll
-        for (int st = 1; st < 8; st <<= 1)
+    for (int st = 1; st < 8; st <<= 1)
+#pragma unroll
+        for (int ps = 0; ps < 2; ++ps)
 #pragma unroll
             for (int j = 0; j < 8; ++j)
                 if (!(j & st)) {
-                    const float a = e[j], b = e[j | st];
-                    e[j] = a + b;
-                    e[j | st] = a - b;
+                    const float a = v[ps][j], b = v[ps][j | st];
+                    v[ps][j] = a + b;
+                    v[ps][j | st] = a - b;
                 }
+    auto lane_stage = [&](auto sc) {
+        constexpr int S = decltype(sc)::value;
+        const float sgn = (i & S) ? -1.f : 1.f;
+        float p[2][8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            float t = e[j];
-            t = __builtin_fmaf(t, (i & 1) ? -1.f : 1.f, dpp_xor<1>(t));
-            t = __builtin_fmaf(t, (i & 2) ? -1.f : 1.f, dpp_xor<2>(t));
-            t = __builtin_fmaf(t, (i & 4) ? -1.f : 1.f, dpp_xor<4>(t));
-            t = __builtin_fmaf(t, (i & 8) ? -1.f : 1.f, dpp_xor<8>(t));
-            e[j] = t * 0.08838834764831844055f;
-        }
+        for (int ps = 0; ps < 2; ++ps)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) p[ps][j] = dpp_xor<S>(v[ps][j]);
+#pragma unroll
+        for (int ps = 0; ps < 2; ++ps)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[ps][j] = __builtin_fmaf(v[ps][j], sgn, p[ps][j]);
+    };
+    lane_stage(std::integral_constant<int, 1>{});
+    lane_stage(std::integral_constant<int, 2>{});
+    lane_stage(std::integral_constant<int, 4>{});
+    lane_stage(std::integral_constant<int, 8>{});
+#pragma unroll
+    for (int ps = 0; ps < 2; ++ps) {
+        const int r = 32 * rb + 8 * wave + 4 * ps + g;
+        float e[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) e[j] = v[ps][j] * 0.08838834764831844055f;
         uint4 out;
         out.x = (uint32_t)float_to_half_bits(e[0]) | ((uint32_t)float_to_half_bits(e[1]) << 16);
         out.y = (uint32_t)float_to_half_bits(e[2]) | ((uint32_t)float_to_half_bits(e[3]) << 16);
@@ -1069,8 +1087,8 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
     auto chunk_prepare = [&](const uint32_t (&w)[2][K], uint32_t (&xb)[2][K]) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const uint32_t p1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)w[h][K - 1], 0x121, 0xF, 0xF, false);
-            const uint32_t p9 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)w[h][K - 1], 0x129, 0xF, 0xF, false);
+            const uint32_t p1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)w[h][K - 1], 0x121, 0xF, 0xF, false);
+            const uint32_t p9 = (uint32_t)__builtin_amdgcn_mov_dpp((int)w[h][K - 1], 0x129, 0xF, 0xF, false);
             xb[h][0] = __builtin_amdgcn_alignbit(first_chunk ? p9 : p1, w[h][0], 16);
 #pragma unroll
             for (int m = 1; m < K; ++m) xb[h][m] = __builtin_amdgcn_alignbit(w[h][m - 1], w[h][m], 16);
