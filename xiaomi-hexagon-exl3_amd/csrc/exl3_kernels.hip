@@ -999,18 +999,26 @@ template <int NE>
 __device__ __forceinline__ void gemm_rows_out(float (&t)[4][NE], int lane, int row0, const uint16_t *svp, int rows,
                                               void *y, int y_f16, size_t y_stride, size_t col0) {
     const int l32 = lane & 31, lh = lane >> 5;
+    // lane stages stage-major over the 4 NE independent values: the DPP reads
+    // and butterflies of one stage issue back to back without wait states
+    auto lane_stage = [&](auto sc) {
+        constexpr int S = decltype(sc)::value;
+        const float sgn = (l32 & S) ? -1.f : 1.f;
+        float p[4][NE];
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
+        for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-        for (int i = 0; i < NE; ++i) {
-            float v = t[cb][i];
-            v = __builtin_fmaf(v, (l32 & 1) ? -1.f : 1.f, lane_xor<1>(v, 0));
-            v = __builtin_fmaf(v, (l32 & 2) ? -1.f : 1.f, lane_xor<2>(v, 0));
-            v = __builtin_fmaf(v, (l32 & 4) ? -1.f : 1.f, lane_xor<4>(v, 0));
-            v = __builtin_fmaf(v, (l32 & 8) ? -1.f : 1.f, lane_xor<8>(v, 0));
-            v = __builtin_fmaf(v, (l32 & 16) ? -1.f : 1.f, lane_xor<16>(v, 0));
-            t[cb][i] = v;
-        }
+            for (int i = 0; i < NE; ++i) p[cb][i] = lane_xor<S>(t[cb][i], 0);
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+            for (int i = 0; i < NE; ++i) t[cb][i] = __builtin_fmaf(t[cb][i], sgn, p[cb][i]);
+    };
+    lane_stage(std::integral_constant<int, 1>{});
+    lane_stage(std::integral_constant<int, 2>{});
+    lane_stage(std::integral_constant<int, 4>{});
+    lane_stage(std::integral_constant<int, 8>{});
+    lane_stage(std::integral_constant<int, 16>{});
 #pragma unroll
     for (int st = 1; st < 4; st <<= 1)
 #pragma unroll
@@ -1025,19 +1033,25 @@ __device__ __forceinline__ void gemm_rows_out(float (&t)[4][NE], int lane, int r
     float svv[4];
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) svv[cb] = half_bits_to_float(svp[32 * cb + l32]);
+    auto store = [&](auto is_f16) {
+        constexpr bool YF16 = decltype(is_f16)::value;
+        typedef typename std::conditional<YF16, uint16_t, float>::type T;
 #pragma unroll
-    for (int i = 0; i < NE; ++i) {
-        const int row = row0 + (i & 3) + 8 * (i >> 2) + 4 * lh;
-        if (row < rows) {
+        for (int i = 0; i < NE; ++i) {
+            const int row = row0 + (i & 3) + 8 * (i >> 2) + 4 * lh;
+            if (row < rows) {
+                T *yr = (T *)y + (size_t)row * y_stride + col0 + l32;
 #pragma unroll
-            for (int cb = 0; cb < 4; ++cb) {
-                const float v = t[cb][i] * 0.08838834764831844055f * svv[cb];
-                const size_t o = (size_t)row * y_stride + col0 + 32 * cb + l32;
-                if (y_f16) ((uint16_t *)y)[o] = float_to_half_bits(v);
-                else ((float *)y)[o] = v;
+                for (int cb = 0; cb < 4; ++cb) {
+                    const float v = t[cb][i] * 0.08838834764831844055f * svv[cb];
+                    if constexpr (YF16) yr[32 * cb] = float_to_half_bits(v);
+                    else yr[32 * cb] = v;
+                }
             }
         }
-    }
+    };
+    if (y_f16) store(std::true_type{});
+    else store(std::false_type{});
 }
 
 template <int K, int CB, int RB>
