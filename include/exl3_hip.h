@@ -99,6 +99,19 @@ exl3_status exl3_hip_mul_mat(const void *records, unsigned bits, unsigned codebo
                              void *y, exl3_dtype yt, size_t y_row_stride,
                              void *workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* y = residual + layer(x): the graph ADD(MUL_MAT(w, x), residual) of
+ * tests/test-exl3-graph.cpp:53-55 in one call, the sum formed in fp32 and
+ * rounded once to yt.  residual: device, rows x n of yt, row stride
+ * residual_row_stride (>= n); it is either y itself with y's stride (an in-place
+ * accumulate) or disjoint from y.  Otherwise as exl3_hip_mul_mat.  The
+ * reference declines this fusion for its kernels (patches/llama-exl3.patch:161-162)
+ * and runs the ADD as a separate graph node. */
+exl3_status exl3_hip_mul_mat_add(const void *records, unsigned bits, unsigned codebook, size_t k, size_t n,
+                                 const void *x, exl3_dtype xt, size_t rows, size_t x_row_stride,
+                                 const void *residual, size_t residual_row_stride,
+                                 void *y, exl3_dtype yt, size_t y_row_stride,
+                                 void *workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* One matrix of an exl3_hip_mul_mat_group call. */
 typedef struct exl3_matrix_desc {
     const void *records;   /* device, (n/128)*(k/128) group records, 16-byte aligned */

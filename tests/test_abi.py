@@ -60,6 +60,13 @@ def test_host_side_status_and_planning():
     assert L.exl3_hip_decode(None, 0, 4, 2, 16, 16, 0, 16, None, None) == 1
     assert L.exl3_hip_get_rows(None, 4, 2, 128, 128, None, 1, None, 0, 128, None, None) == 1
     assert L.exl3_hip_mul_mat_group(None, 1, 4, 2, 2048, None, 1, 1, 2048, 1, None, 0, None) == 1
+    # fused residual add: NULL residual, short residual stride, misaligned residual
+    assert L.exl3_hip_mul_mat_add(None, 4, 2, 128, 128, None, 1, 1, 128, None, 128, 0x100000, 0, 128, None, 0,
+                                  None) == 1
+    assert L.exl3_hip_mul_mat_add(None, 4, 2, 128, 128, None, 1, 1, 128, 0x200000, 64, 0x100000, 0, 128, None, 0,
+                                  None) == 1
+    assert L.exl3_hip_mul_mat_add(None, 4, 2, 128, 128, None, 1, 1, 128, 0x200002, 128, 0x100000, 0, 128, None, 0,
+                                  None) == 1
     import ctypes
     descs = (ctypes.c_size_t * 4)(0, 128, 0, 128)   # one descriptor: NULL records
     assert L.exl3_hip_mul_mat_group(ctypes.cast(descs, ctypes.c_void_p), 0, 4, 2, 128, None, 1, 1, 128, 1,

@@ -114,9 +114,10 @@ exl3_status exl3_hip_workspace_init(void *workspace, size_t workspace_bytes, hip
     return from_hip(exl3k::launch_zero(workspace, workspace_bytes, stream));
 }
 
-exl3_status exl3_hip_mul_mat(const void *records, unsigned bits, unsigned codebook, size_t k, size_t n, const void *x,
-                             exl3_dtype xt, size_t rows, size_t x_row_stride, void *y, exl3_dtype yt,
-                             size_t y_row_stride, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+static exl3_status mul_mat_impl(const void *records, unsigned bits, unsigned codebook, size_t k, size_t n,
+                                const void *x, exl3_dtype xt, size_t rows, size_t x_row_stride, const void *res,
+                                size_t res_row_stride, void *y, exl3_dtype yt, size_t y_row_stride, void *workspace,
+                                size_t workspace_bytes, hipStream_t stream) {
     if (!exl3_hip_supports_mul_mat(bits, codebook, k, n, rows, xt, yt)) return EXL3_INVAL_PARAMS;
     if (!records || !x || !y || !aligned(records, 16)) return EXL3_INVAL_PARAMS;
     if (!aligned(x, dtype_size(xt)) || !aligned(y, dtype_size(yt))) return EXL3_INVAL_PARAMS;
@@ -133,9 +134,36 @@ exl3_status exl3_hip_mul_mat(const void *records, unsigned bits, unsigned codebo
     const int xf = xt == EXL3_F16, yf = yt == EXL3_F16;
     if (gemv)
         return from_hip(exl3k::launch_gemv(records, (int)bits, (int)codebook, k, n, x, xf, rows, x_row_stride, y, yf,
-                                           y_row_stride, workspace, exl3k::gemv_plan(k, n, rows), stream));
+                                           y_row_stride, workspace, exl3k::gemv_plan(k, n, rows), stream, res,
+                                           res_row_stride));
     return from_hip(exl3k::launch_gemm(records, (int)bits, (int)codebook, k, n, x, xf, rows, x_row_stride, y, yf,
-                                       y_row_stride, workspace, exl3k::gemm_plan(k, n, rows), stream));
+                                       y_row_stride, workspace, exl3k::gemm_plan(k, n, rows), stream, res,
+                                       res_row_stride));
+}
+
+exl3_status exl3_hip_mul_mat(const void *records, unsigned bits, unsigned codebook, size_t k, size_t n, const void *x,
+                             exl3_dtype xt, size_t rows, size_t x_row_stride, void *y, exl3_dtype yt,
+                             size_t y_row_stride, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    return mul_mat_impl(records, bits, codebook, k, n, x, xt, rows, x_row_stride, nullptr, 0, y, yt, y_row_stride,
+                        workspace, workspace_bytes, stream);
+}
+
+exl3_status exl3_hip_mul_mat_add(const void *records, unsigned bits, unsigned codebook, size_t k, size_t n,
+                                 const void *x, exl3_dtype xt, size_t rows, size_t x_row_stride, const void *residual,
+                                 size_t residual_row_stride, void *y, exl3_dtype yt, size_t y_row_stride,
+                                 void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (!residual || !y || residual_row_stride < n || !aligned(residual, dtype_size(yt))) return EXL3_INVAL_PARAMS;
+    if (rows && residual != y) {  // the residual is y itself (same stride) or disjoint from it
+        const size_t es = dtype_size(yt);
+        const uintptr_t r0 = (uintptr_t)residual, y0 = (uintptr_t)y;
+        const uintptr_t r1 = r0 + ((rows - 1) * residual_row_stride + n) * es;
+        const uintptr_t y1 = y0 + ((rows - 1) * y_row_stride + n) * es;
+        if (r0 < y1 && y0 < r1) return EXL3_INVAL_PARAMS;
+    } else if (residual_row_stride != y_row_stride) {
+        return EXL3_INVAL_PARAMS;
+    }
+    return mul_mat_impl(records, bits, codebook, k, n, x, xt, rows, x_row_stride, residual, residual_row_stride, y,
+                        yt, y_row_stride, workspace, workspace_bytes, stream);
 }
 
 exl3_status exl3_hip_mul_mat_group(const exl3_matrix_desc *mats, size_t count, unsigned bits, unsigned codebook,

@@ -576,6 +576,8 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
     const uint8_t *records = tg.records[0];
     void *y = tg.y[0];
     size_t y_stride = tg.y_stride[0];
+    const void *res = tg.res[0];
+    size_t res_stride = tg.res_stride[0];
     int nbl = nb;  // column group within the matrix
 #pragma unroll
     for (int i = 1; i < kGemvMaxTargets; ++i)
@@ -583,6 +585,8 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
             records = tg.records[i];
             y = tg.y[i];
             y_stride = tg.y_stride[i];
+            res = tg.res[i];
+            res_stride = tg.res_stride[i];
             nbl = nb - tg.nb_end[i - 1];
         }
     const uint8_t *colgroup = records + (size_t)nbl * kbs * GB;
@@ -762,6 +766,16 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
         a0 *= sv0;
         a1 *= sv1;
         const size_t o = (size_t)rr * y_stride + (size_t)nbl * 128;
+        if (res) {  // fused residual: y = res + layer, one rounding
+            const size_t ro = (size_t)rr * res_stride + (size_t)nbl * 128;
+            if (y_f16) {
+                a0 += half_bits_to_float(((const uint16_t *)res)[ro + lane]);
+                a1 += half_bits_to_float(((const uint16_t *)res)[ro + lane + 64]);
+            } else {
+                a0 += ((const float *)res)[ro + lane];
+                a1 += ((const float *)res)[ro + lane + 64];
+            }
+        }
         if (y_f16) {
             ((uint16_t *)y)[o + lane] = float_to_half_bits(a0);
             ((uint16_t *)y)[o + lane + 64] = float_to_half_bits(a1);
@@ -851,12 +865,14 @@ hipError_t launch_gemv_targets(const GemvTargets &tg, int bits, int cb, const vo
 
 hipError_t launch_gemv(const void *records, int bits, int cb, size_t k, size_t n, const void *x, int x_f16,
                        size_t rows, size_t x_stride, void *y, int y_f16, size_t y_stride, void *workspace,
-                       const GemvPlan &p, hipStream_t stream) {
+                       const GemvPlan &p, hipStream_t stream, const void *res, size_t res_stride) {
     (void)k;
     GemvTargets tg{};
     tg.records[0] = (const uint8_t *)records;
     tg.y[0] = y;
     tg.y_stride[0] = y_stride;
+    tg.res[0] = res;
+    tg.res_stride[0] = res_stride;
     tg.nb_end[0] = (int)(n / 128);
     tg.count = 1;
     return launch_gemv_targets(tg, bits, cb, x, x_f16, rows, x_stride, y_f16, workspace, p, stream);
@@ -997,7 +1013,8 @@ __device__ __forceinline__ int gemm_w_offset(int n, int chunk) {  // halves
 // then 1/sqrt(128) and sv (src/exl3-ggml.cpp:84-90).
 template <int NE>
 __device__ __forceinline__ void gemm_rows_out(float (&t)[4][NE], int lane, int row0, const uint16_t *svp, int rows,
-                                              void *y, int y_f16, size_t y_stride, size_t col0) {
+                                              void *y, int y_f16, size_t y_stride, size_t col0, const void *res,
+                                              size_t res_stride) {
     const int l32 = lane & 31, lh = lane >> 5;
     // lane stages stage-major over the 4 NE independent values: the DPP reads
     // and butterflies of one stage issue back to back without wait states
@@ -1033,32 +1050,43 @@ __device__ __forceinline__ void gemm_rows_out(float (&t)[4][NE], int lane, int r
     float svv[4];
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) svv[cb] = half_bits_to_float(svp[32 * cb + l32]);
-    auto store = [&](auto is_f16) {
-        constexpr bool YF16 = decltype(is_f16)::value;
+    // res (y's dtype): y = res + layer with one rounding of the sum
+    auto store = [&](auto is_f16, auto has_res) {
+        constexpr bool YF16 = decltype(is_f16)::value, RES = decltype(has_res)::value;
         typedef typename std::conditional<YF16, uint16_t, float>::type T;
 #pragma unroll
         for (int i = 0; i < NE; ++i) {
             const int row = row0 + (i & 3) + 8 * (i >> 2) + 4 * lh;
             if (row < rows) {
                 T *yr = (T *)y + (size_t)row * y_stride + col0 + l32;
+                const T *rr = (const T *)res + (size_t)row * res_stride + col0 + l32;
 #pragma unroll
                 for (int cb = 0; cb < 4; ++cb) {
-                    const float v = t[cb][i] * 0.08838834764831844055f * svv[cb];
+                    float v = t[cb][i] * 0.08838834764831844055f * svv[cb];
+                    if constexpr (RES) {
+                        if constexpr (YF16) v += half_bits_to_float(rr[32 * cb]);
+                        else v += rr[32 * cb];
+                    }
                     if constexpr (YF16) yr[32 * cb] = float_to_half_bits(v);
                     else yr[32 * cb] = v;
                 }
             }
         }
     };
-    if (y_f16) store(std::true_type{});
-    else store(std::false_type{});
+    if (res) {
+        if (y_f16) store(std::true_type{}, std::true_type{});
+        else store(std::false_type{}, std::true_type{});
+    } else {
+        if (y_f16) store(std::true_type{}, std::false_type{});
+        else store(std::false_type{}, std::false_type{});
+    }
 }
 
 template <int K, int CB, int RB>
 __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
     const uint8_t *__restrict__ records, int kbs, int nbs, int mtiles, int splits, const uint16_t *__restrict__ xh16,
-    size_t k, uint16_t *__restrict__ partials, void *__restrict__ y, int y_f16,
-    size_t y_stride, int rows) {
+    size_t k, uint16_t *__restrict__ partials, void *y, int y_f16, size_t y_stride, int rows, const void *res,
+    size_t res_stride) {
     constexpr int BM = 32 * RB * kGemmWaves;
     constexpr size_t GB = (size_t)2048 * K + 512;
     __shared__ __attribute__((aligned(16))) uint16_t wlds[2][128 * 128];  // 64 KB
@@ -1257,7 +1285,8 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
         for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
             for (int e = 0; e < 16; ++e) t[cb][e] = acc[rb][cb][e];
-        gemm_rows_out<16>(t, lane, mt * BM + 32 * RB * wave + 32 * rb, svp, rows, y, y_f16, y_stride, (size_t)nb * 128);
+        gemm_rows_out<16>(t, lane, mt * BM + 32 * RB * wave + 32 * rb, svp, rows, y, y_f16, y_stride, (size_t)nb * 128,
+                          res, res_stride);
     }
 }
 
@@ -1269,8 +1298,8 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
 template <int RB>
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(const uint16_t *__restrict__ partials, int splits, int nbs,
                                                           const uint8_t *__restrict__ records, int bits, int kbs,
-                                                          void *__restrict__ y, int y_f16, size_t y_stride, int rows,
-                                                          int nwaves) {
+                                                          void *y, int y_f16, size_t y_stride, int rows,
+                                                          int nwaves, const void *res, size_t res_stride) {
     constexpr int BM = 32 * RB * kGemmWaves;
     constexpr size_t kPerSplit = (size_t)kGemmWaves * RB * 4 * 2 * 64 * 8;  // halves
     const int lane = threadIdx.x & 63;
@@ -1303,7 +1332,8 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const uint16_t *__rest
                 }
     }
     const uint16_t *svp = (const uint16_t *)(records + (size_t)nb * kbs * group_bytes(bits) + 2048 * bits + 256);
-    gemm_rows_out<8>(t, lane, mt * BM + 32 * blk + 16 * vp, svp, rows, y, y_f16, y_stride, (size_t)nb * 128);
+    gemm_rows_out<8>(t, lane, mt * BM + 32 * blk + 16 * vp, svp, rows, y, y_f16, y_stride, (size_t)nb * 128, res,
+                     res_stride);
 }
 
 int gemm_tile_rows(size_t rows) { return rows <= 128 ? 128 : 256; }
@@ -1334,57 +1364,66 @@ GemmPlan gemm_plan(size_t k, size_t n, size_t rows) {
 
 template <int K, int CB>
 static void launch_gemm_kc(const uint8_t *rec, size_t k, uint16_t *xh, size_t rows, void *y, int y_f16,
-                           size_t y_stride, uint8_t *ws, const GemmPlan &p, hipStream_t stream) {
+                           size_t y_stride, uint8_t *ws, const GemmPlan &p, hipStream_t stream, const void *res,
+                           size_t res_stride) {
     const dim3 grid((unsigned)(p.mtiles * p.nbs * p.splits)), block(kGemmWaves * 64);
     uint16_t *part = (uint16_t *)(ws + p.partials_off);
     const int nwaves = p.mtiles * p.nbs * (p.bm / 16);  // reduction: one wave per 16 rows of a tile
     const dim3 rgrid((unsigned)((nwaves + 3) / 4));
     if (p.bm == 128) {
         gemm_kernel<K, CB, 1><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, xh, k, part, y, y_f16,
-                                                          y_stride, (int)rows);
+                                                          y_stride, (int)rows, res, res_stride);
         if (p.splits > 1)
             gemm_reduce_kernel<1><<<rgrid, dim3(256), 0, stream>>>(part, p.splits, p.nbs, rec, K, p.kbs, y, y_f16,
-                                                                   y_stride, (int)rows, nwaves);
+                                                                   y_stride, (int)rows, nwaves, res, res_stride);
     } else {
         gemm_kernel<K, CB, 2><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, xh, k, part, y, y_f16,
-                                                          y_stride, (int)rows);
+                                                          y_stride, (int)rows, res, res_stride);
         if (p.splits > 1)
             gemm_reduce_kernel<2><<<rgrid, dim3(256), 0, stream>>>(part, p.splits, p.nbs, rec, K, p.kbs, y, y_f16,
-                                                                   y_stride, (int)rows, nwaves);
+                                                                   y_stride, (int)rows, nwaves, res, res_stride);
     }
 }
 
 template <int K>
 static hipError_t launch_gemm_k(const void *records, int cb, size_t k, const void *x, int x_f16, size_t rows,
                                 size_t x_stride, void *y, int y_f16, size_t y_stride, uint8_t *ws, const GemmPlan &p,
-                                hipStream_t stream) {
+                                hipStream_t stream, const void *res, size_t res_stride) {
     const uint8_t *rec = (const uint8_t *)records;
     uint16_t *xh = (uint16_t *)(ws + p.xh_off);
     const int rows_padded = p.mtiles * p.bm;
     gemm_xprep_kernel<<<dim3(p.kbs, rows_padded / 32), dim3(256), 0, stream>>>(rec, K, x, x_f16, x_stride, (int)rows,
                                                                                p.kbs, xh);
     switch (cb) {
-    case 0: launch_gemm_kc<K, 0>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream); break;
-    case 1: launch_gemm_kc<K, 1>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream); break;
-    default: launch_gemm_kc<K, 2>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream); break;
+    case 0: launch_gemm_kc<K, 0>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream, res, res_stride); break;
+    case 1: launch_gemm_kc<K, 1>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream, res, res_stride); break;
+    default: launch_gemm_kc<K, 2>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream, res, res_stride); break;
     }
     return hipGetLastError();
 }
 
 hipError_t launch_gemm(const void *records, int bits, int cb, size_t k, size_t n, const void *x, int x_f16,
                        size_t rows, size_t x_stride, void *y, int y_f16, size_t y_stride, void *workspace,
-                       const GemmPlan &p, hipStream_t stream) {
+                       const GemmPlan &p, hipStream_t stream, const void *res, size_t res_stride) {
     (void)n;
     uint8_t *ws = (uint8_t *)workspace;
     switch (bits) {
-    case 1: return launch_gemm_k<1>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
-    case 2: return launch_gemm_k<2>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
-    case 3: return launch_gemm_k<3>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
-    case 4: return launch_gemm_k<4>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
-    case 5: return launch_gemm_k<5>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
-    case 6: return launch_gemm_k<6>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
-    case 7: return launch_gemm_k<7>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
-    default: return launch_gemm_k<8>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream);
+    case 1: return launch_gemm_k<1>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream, res,
+                                       res_stride);
+    case 2: return launch_gemm_k<2>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream, res,
+                                       res_stride);
+    case 3: return launch_gemm_k<3>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream, res,
+                                       res_stride);
+    case 4: return launch_gemm_k<4>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream, res,
+                                       res_stride);
+    case 5: return launch_gemm_k<5>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream, res,
+                                       res_stride);
+    case 6: return launch_gemm_k<6>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream, res,
+                                       res_stride);
+    case 7: return launch_gemm_k<7>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream, res,
+                                       res_stride);
+    default: return launch_gemm_k<8>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream, res,
+                                       res_stride);
     }
 }
 

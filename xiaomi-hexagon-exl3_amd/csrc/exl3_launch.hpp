@@ -30,6 +30,8 @@ struct GemvTargets {
     const uint8_t *records[kGemvMaxTargets];
     void *y[kGemvMaxTargets];
     size_t y_stride[kGemvMaxTargets];
+    const void *res[kGemvMaxTargets];  // optional residual added to y (y's dtype), or null
+    size_t res_stride[kGemvMaxTargets];
     int nb_end[kGemvMaxTargets];
     int count;
 };
@@ -47,14 +49,16 @@ GemvPlan gemv_plan(size_t k, size_t n, size_t rows);
 GemmPlan gemm_plan(size_t k, size_t n, size_t rows);
 int gemm_tile_rows(size_t rows);
 
+// res (optional, y's dtype, row stride res_stride): y = res + layer(x), the sum
+// rounded once; res may be y itself (same stride)
 hipError_t launch_gemv(const void *records, int bits, int cb, size_t k, size_t n, const void *x, int x_f16,
                        size_t rows, size_t x_stride, void *y, int y_f16, size_t y_stride, void *workspace,
-                       const GemvPlan &plan, hipStream_t stream);
+                       const GemvPlan &plan, hipStream_t stream, const void *res = nullptr, size_t res_stride = 0);
 hipError_t launch_gemv_targets(const GemvTargets &targets, int bits, int cb, const void *x, int x_f16, size_t rows,
                                size_t x_stride, int y_f16, void *workspace, const GemvPlan &plan, hipStream_t stream);
 hipError_t launch_gemm(const void *records, int bits, int cb, size_t k, size_t n, const void *x, int x_f16,
                        size_t rows, size_t x_stride, void *y, int y_f16, size_t y_stride, void *workspace,
-                       const GemmPlan &plan, hipStream_t stream);
+                       const GemmPlan &plan, hipStream_t stream, const void *res = nullptr, size_t res_stride = 0);
 hipError_t launch_decode(const void *src, int records_layout, int bits, int cb, size_t k, size_t n,
                          size_t first, size_t count, uint16_t *out, hipStream_t stream);
 hipError_t launch_reconstruct(const void *src, int records_layout, const uint16_t *su, const uint16_t *sv,

@@ -20,7 +20,7 @@ EXPORTS = [
     "exl3_hip_mul_mat_workspace_bytes", "exl3_hip_workspace_init", "exl3_hip_mul_mat", "exl3_hip_decode",
     "exl3_hip_reconstruct", "exl3_hip_get_rows", "exl3_hip_codebook", "exl3_hip_hadamard128",
     "exl3_hip_pack_records", "exl3_hip_validate_records",
-    "exl3_hip_mul_mat_group",
+    "exl3_hip_mul_mat_group", "exl3_hip_mul_mat_add",
     "exl3_hip_model_open", "exl3_hip_model_close", "exl3_hip_model_tensor_count", "exl3_hip_model_payload_bytes",
     "exl3_hip_model_hidden_size", "exl3_hip_model_vocab_size", "exl3_hip_model_bits_per_weight",
     "exl3_hip_model_embedding", "exl3_hip_model_matrix_count", "exl3_hip_model_matrix", "exl3_hip_model_record_bytes",
@@ -53,6 +53,8 @@ def load(path=LIB_PATH):
     L.exl3_hip_workspace_init.argtypes = [vp, sz, st]
     L.exl3_hip_mul_mat.restype = i
     L.exl3_hip_mul_mat.argtypes = [vp, u, u, sz, sz, vp, i, sz, sz, vp, i, sz, vp, sz, st]
+    L.exl3_hip_mul_mat_add.restype = i
+    L.exl3_hip_mul_mat_add.argtypes = [vp, u, u, sz, sz, vp, i, sz, sz, vp, sz, vp, i, sz, vp, sz, st]
     L.exl3_hip_mul_mat_group.restype = i
     L.exl3_hip_mul_mat_group.argtypes = [vp, sz, u, u, sz, vp, i, sz, sz, i, vp, sz, st]
     L.exl3_hip_decode.restype = i
@@ -127,19 +129,29 @@ def new_workspace(k, n, rows, device="cuda"):
     return ws
 
 
-def mul_mat(records, bits, k, n, x, codebook=CB_MUL1, out_dtype=None, y=None, workspace=None, stream=None):
-    """y = EXL3 linear layer applied to x ([rows, k] fp16/fp32 CUDA tensor, row stride x.stride(0))."""
+def mul_mat(records, bits, k, n, x, codebook=CB_MUL1, out_dtype=None, y=None, workspace=None, stream=None,
+            residual=None):
+    """y = EXL3 linear layer applied to x ([rows, k] fp16/fp32 CUDA tensor, row stride x.stride(0)).
+    residual ([rows, n], y's dtype; may be y itself): y = residual + layer(x) in one call
+    (exl3_hip_mul_mat_add)."""
     import torch
     assert x.dim() == 2 and x.stride(1) == 1 and x.dtype in (torch.float16, torch.float32)
     rows = x.shape[0]
     if y is None:
-        y = torch.empty((rows, n), dtype=out_dtype or torch.float32, device=x.device)
+        dt = out_dtype or (residual.dtype if residual is not None else torch.float32)
+        y = torch.empty((rows, n), dtype=dt, device=x.device)
     assert y.dim() == 2 and y.stride(1) == 1 and y.dtype in (torch.float16, torch.float32)
     xt = F16 if x.dtype == torch.float16 else F32
     yt = F16 if y.dtype == torch.float16 else F32
     ws_ptr, ws_bytes = (None, 0) if workspace is None else (_ptr(workspace), workspace.numel())
-    _check(lib().exl3_hip_mul_mat(_ptr(records), bits, codebook, k, n, _ptr(x), xt, rows, x.stride(0), _ptr(y), yt,
-                                  y.stride(0), ws_ptr, ws_bytes, _stream(stream)), "mul_mat")
+    if residual is None:
+        _check(lib().exl3_hip_mul_mat(_ptr(records), bits, codebook, k, n, _ptr(x), xt, rows, x.stride(0), _ptr(y),
+                                      yt, y.stride(0), ws_ptr, ws_bytes, _stream(stream)), "mul_mat")
+        return y
+    assert residual.dim() == 2 and residual.stride(1) == 1 and residual.dtype == y.dtype
+    _check(lib().exl3_hip_mul_mat_add(_ptr(records), bits, codebook, k, n, _ptr(x), xt, rows, x.stride(0),
+                                      _ptr(residual), residual.stride(0), _ptr(y), yt, y.stride(0), ws_ptr, ws_bytes,
+                                      _stream(stream)), "mul_mat_add")
     return y
 
 
