@@ -2,6 +2,7 @@
 with the golden vectors of the compiled reference codec."""
 import hashlib
 import json
+import subprocess
 from pathlib import Path
 
 import numpy as np
@@ -111,3 +112,14 @@ def test_decode_mixed_rates(amd, oracle, bits):
     p = synth.packed_tiles(bits * 7, k, n, bits)
     out = host_u16(amd.decode(dev(p), bits, k, n, codebook=2))
     assert np.array_equal(out, oracle.decode_inner(p, k, n, bits, 2))
+
+
+def test_cpp_codec_api_program():
+    """tests/cpp/test_codec_api.cpp: the C++ API (include/exl3_codec.h) driven
+    like the reference's tests/test_codec.cpp, as a separate program built by
+    build() against the in-tree library."""
+    exe = Path(__file__).resolve().parent / "cpp" / "test_codec_api"
+    assert exe.exists(), "tests/cpp/test_codec_api is built by __graft_entry__.build()"
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
+    print(r.stdout, r.stderr, flush=True)
+    assert r.returncode == 0 and "PASS" in r.stdout
