@@ -4,6 +4,8 @@ and further malformed inputs on the CPU; embeddings and record uploads on the GP
 against the oracle."""
 import copy
 import struct
+import subprocess
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -180,3 +182,15 @@ def test_upload_records_feed_the_layer(tmp_path, amd, oracle):
             x = synth.activations(93 + idx, 3, k)
             y = amd.mul_mat(rec, bits, k, n, torch.from_numpy(x).cuda(), codebook=cb).cpu().numpy()
             assert_layer_close(y, oracle.mul_mat(want, bits, cb, k, n, x), what=prefix)
+
+
+@pytest.mark.gpu
+def test_cpp_model_api_program(tmp_path):
+    """tests/cpp/test_model_api.cpp: exl3::Model through its C++ class, as the
+    reference's tests/test_model_reader.cpp drives its own (known-answer tied
+    embedding, row cache, token bound, four rejections)."""
+    exe = Path(__file__).resolve().parent / "cpp" / "test_model_api"
+    assert exe.exists(), "tests/cpp/test_model_api is built by __graft_entry__.build()"
+    r = subprocess.run([str(exe), str(tmp_path)], capture_output=True, text=True, timeout=300)
+    print(r.stdout, r.stderr, flush=True)
+    assert r.returncode == 0 and "PASS" in r.stdout
