@@ -141,6 +141,22 @@ exl3_status exl3_hip_decode(const void *src, exl3_layout layout, unsigned bits, 
                             size_t k, size_t n, size_t first_column, size_t column_count,
                             uint16_t *out, hipStream_t stream);
 
+/* One matrix of an exl3_hip_decode_batch call. */
+typedef struct exl3_decode_desc {
+    const void *src;   /* device, packed weights in the call's layout, 16-byte aligned */
+    size_t k, n;       /* shape (multiples of 16 for UPSTREAM_TILES, of 128 for RECORDS) */
+    uint16_t *out;     /* device, row-major fp16 bits out[k][n], 16-byte aligned */
+    unsigned bits;     /* 1..8 */
+} exl3_decode_desc;
+
+/* exl3_hip_decode of whole matrices, many per launch: the matrices of one rate
+ * share a launch (up to 32 each), so a model's weight set decodes in a few
+ * launches instead of one per tensor; output bit-identical to exl3_hip_decode.
+ * count 0 is a no-op.  This entry point has no counterpart in the reference,
+ * which decodes one tensor per decode_inner call (src/exl3_codec.cpp:117-145). */
+exl3_status exl3_hip_decode_batch(const exl3_decode_desc *descs, size_t count, exl3_layout layout,
+                                  unsigned codebook, hipStream_t stream);
+
 /* Original-basis weights diag(su) H W_hat H diag(sv) as fp16 bits out[k][column_count],
  * bit-exact with exl3::reconstruct_slice.  UPSTREAM_TILES takes su (k) and sv (n)
  * fp16 device vectors; RECORDS reads them from the records (su/sv may be NULL).

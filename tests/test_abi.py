@@ -78,6 +78,13 @@ def test_host_side_status_and_planning():
     assert L.exl3_hip_get_rows(None, 4, 2, 100, 128, None, 1, None, 0, 128, None, None) == 1
     assert L.exl3_hip_get_rows(None, 4, 2, 128, 128, None, 0, None, 0, 128, None, None) == 0  # count 0: no-op
     assert L.exl3_hip_hadamard128(None, 100, None) == 1
+    assert L.exl3_hip_decode_batch(None, 0, 0, 2, None) == 0        # nothing to decode
+    assert L.exl3_hip_decode_batch(None, 1, 0, 2, None) == 1        # NULL descriptors
+    assert L.exl3_hip_decode_batch(None, 0, 7, 2, None) == 1        # unknown layout
+    bad = (ctypes.c_size_t * 5)(0x10000, 16, 16, 0x20000, 9)        # bits 9
+    assert L.exl3_hip_decode_batch(ctypes.cast(bad, ctypes.c_void_p), 1, 0, 2, None) == 1
+    bad = (ctypes.c_size_t * 5)(0x10000, 16, 24, 0x20000, 4)        # n not a multiple of 16
+    assert L.exl3_hip_decode_batch(ctypes.cast(bad, ctypes.c_void_p), 1, 0, 2, None) == 1
     assert L.exl3_hip_status_string(3) == b"workspace too small"
 
 

@@ -123,3 +123,44 @@ def test_cpp_codec_api_program():
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
     print(r.stdout, r.stderr, flush=True)
     assert r.returncode == 0 and "PASS" in r.stdout
+
+
+def test_decode_batch_matches_single_decodes(amd, oracle):
+    """exl3_hip_decode_batch: 45 matrices of every rate (more than one launch's
+    32 for 4 bits), upstream tiles, each bit-identical with its own
+    exl3_hip_decode call; the small ones also with the oracle."""
+    import torch
+    g = torch.Generator(device="cuda")
+    shapes = [(16, 16), (32, 48), (128, 128), (256, 512), (2048, 128), (128, 2064), (640, 784)]
+    items, meta = [], []
+    for j in range(45):
+        bits = 4 if j >= 13 else 1 + j % 8
+        k, n = shapes[j % len(shapes)]
+        g.manual_seed(500 + j)
+        p = torch.randint(-32768, 32768, (k * n * bits // 16,), generator=g, device="cuda",
+                          dtype=torch.int32).to(torch.int16)
+        items.append((p, bits, k, n, None))
+        meta.append((p, bits, k, n))
+    outs = amd.decode_batch(items, codebook=2)
+    torch.cuda.synchronize()
+    for (p, bits, k, n), out in zip(meta, outs):
+        single = amd.decode(p, bits, k, n, codebook=2)
+        torch.cuda.synchronize()
+        assert torch.equal(out, single), (bits, k, n)
+        if k * n <= 128 * 128:
+            want = oracle.decode_inner(p.cpu().numpy().view(np.uint16), k, n, bits, 2)
+            assert np.array_equal(host_u16(out), want), (bits, k, n)
+    assert amd.decode_batch([], codebook=2) == []
+
+
+def test_decode_batch_records_layout(amd):
+    import torch
+    items = []
+    for j, (k, n, bits) in enumerate([(128, 256, 3), (256, 128, 6), (384, 384, 3), (128, 128, 2)]):
+        rec = synth.pack_records(synth.packed_tiles(610 + j, k, n, bits), *synth.layer_scales(610 + j, k, n), bits)
+        items.append((dev(rec.view(np.uint8)), bits, k, n, None))
+    outs = amd.decode_batch(items, codebook=1, layout=amd.LAYOUT_RECORDS)
+    for (rd, bits, k, n, _), out in zip(items, outs):
+        single = amd.decode(rd, bits, k, n, codebook=1, layout=amd.LAYOUT_RECORDS)
+        torch.cuda.synchronize()
+        assert torch.equal(out, single), (bits, k, n)

@@ -210,6 +210,51 @@ exl3_status exl3_hip_mul_mat_group(const exl3_matrix_desc *mats, size_t count, u
                                                yt == EXL3_F16, workspace, exl3k::gemv_plan(k, n_total, rows), stream));
 }
 
+exl3_status exl3_hip_decode_batch(const exl3_decode_desc *descs, size_t count, exl3_layout layout,
+                                  unsigned codebook, hipStream_t stream) {
+    if (layout != EXL3_LAYOUT_RECORDS && layout != EXL3_LAYOUT_UPSTREAM_TILES) return EXL3_INVAL_PARAMS;
+    if (count && !descs) return EXL3_INVAL_PARAMS;
+    const size_t mult = layout == EXL3_LAYOUT_RECORDS ? 128 : 16;
+    for (size_t i = 0; i < count; ++i) {
+        const exl3_decode_desc &d = descs[i];
+        if (!valid_rate(d.bits, codebook) || !d.src || !d.out || !aligned(d.src, 16) || !aligned(d.out, 16) ||
+            !valid_matrix(d.k, d.n, mult) || (d.k / 16) * ((d.n / 16 + 15) / 16) > (size_t)0x7fffffff)
+            return EXL3_INVAL_PARAMS;
+    }
+    // one launch per (rate, up to kDecodeBatchMax matrices); matrices keep their order within a rate
+    const int rl = layout == EXL3_LAYOUT_RECORDS;
+    for (unsigned bits = 1; bits <= 8; ++bits) {
+        exl3k::DecodeBatch b{};
+        size_t wgs = 0;
+        auto flush = [&]() -> exl3_status {
+            if (!b.count) return EXL3_OK;
+            const hipError_t e = exl3k::launch_decode_batch(b, rl, (int)bits, (int)codebook, (unsigned)wgs, stream);
+            b = exl3k::DecodeBatch{};
+            wgs = 0;
+            return from_hip(e);
+        };
+        for (size_t i = 0; i < count; ++i) {
+            const exl3_decode_desc &d = descs[i];
+            if (d.bits != bits) continue;
+            const size_t mwgs = (d.k / 16) * ((d.n / 16 + 15) / 16);
+            if (b.count == exl3k::kDecodeBatchMax || wgs + mwgs > (size_t)0x7fffffff) {
+                const exl3_status st = flush();
+                if (st != EXL3_OK) return st;
+            }
+            b.src[b.count] = d.src;
+            b.out[b.count] = d.out;
+            b.k[b.count] = d.k;
+            b.n[b.count] = d.n;
+            b.wg_begin[b.count] = (unsigned)wgs;
+            ++b.count;
+            wgs += mwgs;
+        }
+        const exl3_status st = flush();
+        if (st != EXL3_OK) return st;
+    }
+    return EXL3_OK;
+}
+
 exl3_status exl3_hip_decode(const void *src, exl3_layout layout, unsigned bits, unsigned codebook, size_t k, size_t n,
                             size_t first_column, size_t column_count, uint16_t *out, hipStream_t stream) {
     if (!valid_rate(bits, codebook) || !src || !out || !aligned(src, 16) || !aligned(out, 16)) return EXL3_INVAL_PARAMS;

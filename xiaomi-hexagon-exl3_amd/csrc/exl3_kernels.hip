@@ -152,17 +152,17 @@ hipError_t launch_zero(void *ptr, size_t bytes, hipStream_t stream) {
 }
 
 // ============================================================== decode
-// One workgroup: one 16-row tile row rk, 16 consecutive tile columns.
-// Lane (wave w, lane l): tile w*4 + l/16, run c = l%8, h = (l%16)/8.
+// One workgroup block: one 16-row tile row rk, 16 consecutive tile columns
+// starting at tile bx * 16 of the slice.  Lane (wave w, lane l): tile w*4 + l/16,
+// run c = l%8, h = (l%16)/8.
+constexpr int kDecodePitch = 16 * 16 + 8;
 template <int K, int CB>
-__global__ __launch_bounds__(256) void decode_kernel(const uint8_t *__restrict__ src, int records_layout, size_t k,
-                                                     size_t n, size_t first_tile, size_t tile_count,
-                                                     uint16_t *__restrict__ out) {
-    constexpr int PITCH = 16 * 16 + 8;
-    __shared__ uint16_t tb[16 * PITCH];
+__device__ __forceinline__ void decode_block(const uint8_t *__restrict__ src, int records_layout, size_t k, size_t n,
+                                             size_t first_tile, size_t tile_count, uint16_t *__restrict__ out,
+                                             size_t bx, size_t rk, uint16_t *tb) {
+    constexpr int PITCH = kDecodePitch;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const size_t rk = blockIdx.y;
-    const size_t t0 = (size_t)blockIdx.x * 16;  // first tile (relative to first_tile) of this workgroup
+    const size_t t0 = bx * 16;  // first tile (relative to first_tile) of this workgroup
     const int tl = wave * 4 + (lane >> 4);
     const int c = lane & 7, h = (lane >> 3) & 1;
     if (t0 + tl < tile_count) {
@@ -195,6 +195,30 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t *__restrict__
     }
 }
 
+template <int K, int CB>
+__global__ __launch_bounds__(256) void decode_kernel(const uint8_t *__restrict__ src, int records_layout, size_t k,
+                                                     size_t n, size_t first_tile, size_t tile_count,
+                                                     uint16_t *__restrict__ out) {
+    __shared__ uint16_t tb[16 * kDecodePitch];
+    decode_block<K, CB>(src, records_layout, k, n, first_tile, tile_count, out, blockIdx.x, blockIdx.y, tb);
+}
+
+// Several whole matrices of one rate in one launch: workgroup w belongs to the
+// matrix m whose range [wg_begin[m], wg_begin[m + 1]) holds it, and decodes its
+// block (bx, rk) = (local % gx, local / gx) with gx = ceil(n / 256).
+template <int K, int CB>
+__global__ __launch_bounds__(256) void decode_batch_kernel(DecodeBatch batch, int records_layout) {
+    __shared__ uint16_t tb[16 * kDecodePitch];
+    const unsigned w = blockIdx.x;
+    int m = 0;
+    for (int i = 1; i < batch.count; ++i)
+        if (w >= batch.wg_begin[i]) m = i;
+    const size_t k = batch.k[m], n = batch.n[m];
+    const size_t gx = (n / 16 + 15) / 16, local = w - batch.wg_begin[m];
+    decode_block<K, CB>((const uint8_t *)batch.src[m], records_layout, k, n, 0, n / 16, batch.out[m], local % gx,
+                        local / gx, tb);
+}
+
 template <int K>
 static hipError_t launch_decode_k(const void *src, int rl, int cb, size_t k, size_t n, size_t first, size_t count,
                                   uint16_t *out, hipStream_t stream) {
@@ -207,6 +231,29 @@ static hipError_t launch_decode_k(const void *src, int rl, int cb, size_t k, siz
     default: decode_kernel<K, 2><<<grid, block, 0, stream>>>(s, rl, k, n, first / 16, tiles, out); break;
     }
     return hipGetLastError();
+}
+
+template <int K>
+static hipError_t launch_decode_batch_k(const DecodeBatch &b, int rl, int cb, unsigned wgs, hipStream_t stream) {
+    switch (cb) {
+    case 0: decode_batch_kernel<K, 0><<<dim3(wgs), dim3(256), 0, stream>>>(b, rl); break;
+    case 1: decode_batch_kernel<K, 1><<<dim3(wgs), dim3(256), 0, stream>>>(b, rl); break;
+    default: decode_batch_kernel<K, 2><<<dim3(wgs), dim3(256), 0, stream>>>(b, rl); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_batch(const DecodeBatch &b, int rl, int bits, int cb, unsigned wgs, hipStream_t stream) {
+    switch (bits) {
+    case 1: return launch_decode_batch_k<1>(b, rl, cb, wgs, stream);
+    case 2: return launch_decode_batch_k<2>(b, rl, cb, wgs, stream);
+    case 3: return launch_decode_batch_k<3>(b, rl, cb, wgs, stream);
+    case 4: return launch_decode_batch_k<4>(b, rl, cb, wgs, stream);
+    case 5: return launch_decode_batch_k<5>(b, rl, cb, wgs, stream);
+    case 6: return launch_decode_batch_k<6>(b, rl, cb, wgs, stream);
+    case 7: return launch_decode_batch_k<7>(b, rl, cb, wgs, stream);
+    default: return launch_decode_batch_k<8>(b, rl, cb, wgs, stream);
+    }
 }
 
 hipError_t launch_decode(const void *src, int rl, int bits, int cb, size_t k, size_t n, size_t first, size_t count,

@@ -36,6 +36,16 @@ struct GemvTargets {
     int count;
 };
 
+// Whole matrices of one rate decoded by one launch (decode_batch_kernel).
+constexpr int kDecodeBatchMax = 32;
+struct DecodeBatch {
+    const void *src[kDecodeBatchMax];
+    uint16_t *out[kDecodeBatchMax];
+    size_t k[kDecodeBatchMax], n[kDecodeBatchMax];
+    unsigned wg_begin[kDecodeBatchMax];  // first workgroup of each matrix; (k/16) * ceil(n/256) each
+    int count;
+};
+
 struct GemvPlan {
     int nbs, kbs, splits, nkw;  // nkw: largest kb count of a split
     size_t counters_off, dummy_off, partials_off, bytes;
@@ -61,6 +71,8 @@ hipError_t launch_gemm(const void *records, int bits, int cb, size_t k, size_t n
                        const GemmPlan &plan, hipStream_t stream, const void *res = nullptr, size_t res_stride = 0);
 hipError_t launch_decode(const void *src, int records_layout, int bits, int cb, size_t k, size_t n,
                          size_t first, size_t count, uint16_t *out, hipStream_t stream);
+hipError_t launch_decode_batch(const DecodeBatch &batch, int records_layout, int bits, int cb, unsigned workgroups,
+                               hipStream_t stream);
 hipError_t launch_reconstruct(const void *src, int records_layout, const uint16_t *su, const uint16_t *sv,
                               int bits, int cb, size_t k, size_t n, size_t first, size_t count, uint16_t *out,
                               hipStream_t stream);

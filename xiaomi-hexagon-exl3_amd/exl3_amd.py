@@ -20,7 +20,7 @@ EXPORTS = [
     "exl3_hip_mul_mat_workspace_bytes", "exl3_hip_workspace_init", "exl3_hip_mul_mat", "exl3_hip_decode",
     "exl3_hip_reconstruct", "exl3_hip_get_rows", "exl3_hip_codebook", "exl3_hip_hadamard128",
     "exl3_hip_pack_records", "exl3_hip_validate_records",
-    "exl3_hip_mul_mat_group", "exl3_hip_mul_mat_add",
+    "exl3_hip_mul_mat_group", "exl3_hip_mul_mat_add", "exl3_hip_decode_batch",
     "exl3_hip_model_open", "exl3_hip_model_close", "exl3_hip_model_tensor_count", "exl3_hip_model_payload_bytes",
     "exl3_hip_model_hidden_size", "exl3_hip_model_vocab_size", "exl3_hip_model_bits_per_weight",
     "exl3_hip_model_embedding", "exl3_hip_model_matrix_count", "exl3_hip_model_matrix", "exl3_hip_model_record_bytes",
@@ -54,6 +54,8 @@ def load(path=LIB_PATH):
     L.exl3_hip_mul_mat.restype = i
     L.exl3_hip_mul_mat.argtypes = [vp, u, u, sz, sz, vp, i, sz, sz, vp, i, sz, vp, sz, st]
     L.exl3_hip_mul_mat_add.restype = i
+    L.exl3_hip_decode_batch.restype = i
+    L.exl3_hip_decode_batch.argtypes = [vp, sz, i, u, st]
     L.exl3_hip_mul_mat_add.argtypes = [vp, u, u, sz, sz, vp, i, sz, sz, vp, sz, vp, i, sz, vp, sz, st]
     L.exl3_hip_mul_mat_group.restype = i
     L.exl3_hip_mul_mat_group.argtypes = [vp, sz, u, u, sz, vp, i, sz, sz, i, vp, sz, st]
@@ -192,6 +194,26 @@ def decode(src, bits, k, n, codebook=CB_MUL1, layout=LAYOUT_UPSTREAM_TILES, firs
     _check(lib().exl3_hip_decode(_ptr(src), layout, bits, codebook, k, n, first, count, _ptr(out), _stream(stream)),
            "decode")
     return out
+
+
+class _DecodeDesc(ctypes.Structure):
+    _fields_ = [("src", ctypes.c_void_p), ("k", ctypes.c_size_t), ("n", ctypes.c_size_t),
+                ("out", ctypes.c_void_p), ("bits", ctypes.c_uint)]
+
+
+def decode_batch(items, codebook=CB_MUL1, layout=LAYOUT_UPSTREAM_TILES, stream=None):
+    """items: [(src, bits, k, n, out)] with out an int16 tensor [k, n] (or None to allocate).
+    Decodes every matrix (exl3_hip_decode_batch); returns the outputs."""
+    import torch
+    outs, descs = [], (_DecodeDesc * max(1, len(items)))()
+    for j, (src, bits, k, n, out) in enumerate(items):
+        if out is None:
+            out = torch.empty((k, n), dtype=torch.int16, device=src.device)
+        outs.append(out)
+        descs[j] = _DecodeDesc(src.data_ptr(), k, n, out.data_ptr(), bits)
+    _check(lib().exl3_hip_decode_batch(ctypes.cast(descs, ctypes.c_void_p), len(items), layout, codebook,
+                                       _stream(stream)), "decode_batch")
+    return outs
 
 
 def reconstruct(src, bits, k, n, su=None, sv=None, codebook=CB_MUL1, layout=LAYOUT_UPSTREAM_TILES, first=0,
