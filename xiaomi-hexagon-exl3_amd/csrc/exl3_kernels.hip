@@ -566,7 +566,7 @@ template <int K>
 struct GemvStream {
     static constexpr int DEPTH = K <= 2 ? 12 : (K <= 4 ? 8 : 4);  // groups in flight per wave
 };
-constexpr int kGemvPrepMax = 16;          // (kb, row) prep blocks per wave
+constexpr int kGemvPrepMax = 16;          // a workgroup preps at most kGemvPrepMax x waves (kb, row) blocks
 constexpr size_t kGemvDummyBytes = 8192;  // >= largest lane offset of a group + its K words (1024 K)
 constexpr size_t kGemvFragLds = 49152;    // LDS budget of the B fragments of a workgroup
 
@@ -655,62 +655,134 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
     };
     uint32_t buf[D][K];
 
-    // 1. loads: the activation pair and su pair of each of this wave's (kb, row)
-    // prep blocks blk = wave + W q.  NQ (slots per wave) is a compile-time bound
-    // and a slot past the last block re-reads that block (never used), so the
-    // loads are straight-line code and all in flight together: with a branch per
-    // slot the compiler pulls each conversion up to its load and waits there,
-    // one round trip per slot.
-    // 2. prep arithmetic: x su, H128 per (kb, row), hi/lo fp16 pairs into the
-    // fragment blocks.  Element 2 lane (+1) of block kb is tile row lane / 8 (r4 = lane / 32,
-    // kg = lane / 8 % 4), rows 2 (lane % 8) (+1): half (lane / 4) % 2, fragment
-    // elements 2 (lane % 4) (+1).
+    // 1-2. prep: xh = H128(x[r] su) per (kb, row) block of the workgroup, as
+    // fp16 hi = rn(xh) and lo = rn(xh - hi) into the B fragments.  Unit q of
+    // wave w is up to four blocks (block = kbl rows + r): lane 16 g + i holds
+    // elements 8 i .. 8 i + 7 of block (4 q + g) W + w (blocks dealt across the
+    // waves first, so a few blocks still run on as many waves): H128 stages 1,
+    // 2, 4 inside the lane, 8 .. 64 across lanes i ^ 1 .. 8 by DPP, in the
+    // reference's stage order.
+    // Elements 8 i .. 8 i + 7 are one 16-byte slot of the fragment blocks (tile
+    // row 4 (i / 8) + (i / 2) % 4 ... : r4 = i / 8, kg = (i / 2) % 4, half = i % 2),
+    // so a lane stores hi and lo with one 16-byte write each.  NQ (units per
+    // wave) is a compile-time bound, and a block past the last re-reads the last
+    // block (never stored), so the loads are straight-line code and all in
+    // flight together.
     const int nblk = nkb * rows;
     auto prologue = [&](auto nq_c, auto is_f16) {
         constexpr int NQ = decltype(nq_c)::value;
         constexpr bool XF16 = decltype(is_f16)::value;
-        uint32_t px0[NQ], px1[NQ], ps[NQ];
+        const int pi = lane & 15;
+        uint4 xr[NQ][XF16 ? 1 : 2], sr[NQ];
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
-            const int blk = wave + q * W < nblk ? wave + q * W : nblk - 1;
+            const int bu = (4 * q + g) * W + wave;
+            const int blk = bu < nblk ? bu : nblk - 1;
             const int kbl = blk / rows, r = blk - kbl * rows;
             const int kb = kb0 + kbl;
-            ps[q] = ((const uint32_t *)(records + (size_t)kb * GB + 2048 * K))[lane];  // record (0, kb): su pair
-            const size_t xi = (size_t)r * x_stride + (size_t)kb * 128 + 2 * lane;
-            if constexpr (XF16) {
-                px0[q] = ((const uint16_t *)x)[xi];
-                px1[q] = ((const uint16_t *)x)[xi + 1];
-            } else {
-                px0[q] = ((const uint32_t *)x)[xi];
-                px1[q] = ((const uint32_t *)x)[xi + 1];
-            }
+            sr[q] = *(const uint4 *)(records + (size_t)kb * GB + 2048 * K + 16 * pi);  // record (0, kb): su
+            const size_t xi = (size_t)r * x_stride + (size_t)kb * 128 + 8 * pi;
+            // element alignment only (any row stride): the compiler emits unaligned vector loads
+            if constexpr (XF16) __builtin_memcpy(&xr[q][0], (const uint16_t *)x + xi, 16);
+            else __builtin_memcpy(&xr[q][0], (const float *)x + xi, 32);
         }
-        const int r4 = lane >> 5, kg = (lane >> 3) & 3, half = (lane >> 2) & 1, jj = 2 * (lane & 3);
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
-            const int blk = wave + q * W;
-            if (blk < nblk) {
-                const int kbl = blk / rows, r = blk - kbl * rows;
-                const float x0 = XF16 ? half_bits_to_float((uint16_t)px0[q]) : bitcast<float>(px0[q]);
-                const float x1 = XF16 ? half_bits_to_float((uint16_t)px1[q]) : bitcast<float>(px1[q]);
-                float a = x0 * half_bits_to_float((uint16_t)(ps[q] & 0xffffu));
-                float b = x1 * half_bits_to_float((uint16_t)(ps[q] >> 16));
-                h128_pair(a, b, lane);
-                const _Float16 ha = (_Float16)a, hb = (_Float16)b;
-                const h2 hi = {ha, hb}, lo = {(_Float16)(a - (float)ha), (_Float16)(b - (float)hb)};
-                uint8_t *bp = frag + (size_t)((kbl * 2 + r4) * 2 + half) * blk_bytes + jj * 2;
-                *(h2 *)(bp + ((kg * 2 + 0) * rows + r) * 16) = hi;
-                *(h2 *)(bp + ((kg * 2 + 1) * rows + r) * 16) = lo;
+            if (4 * q * W + wave < nblk) {  // uniform in the wave: the DPP stages see every lane
+                const uint32_t sw[4] = {sr[q].x, sr[q].y, sr[q].z, sr[q].w};
+                float v[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    float xv;
+                    if constexpr (XF16) {
+                        const uint4 &w4 = xr[q][0];
+                        const uint32_t wd = (j >> 1) == 0 ? w4.x : (j >> 1) == 1 ? w4.y : (j >> 1) == 2 ? w4.z : w4.w;
+                        xv = half_bits_to_float((uint16_t)(wd >> (16 * (j & 1))));
+                    } else {
+                        const uint4 &w4 = xr[q][j >> 2];
+                        const uint32_t wd = (j & 3) == 0 ? w4.x : (j & 3) == 1 ? w4.y : (j & 3) == 2 ? w4.z : w4.w;
+                        xv = __uint_as_float(wd);
+                    }
+                    v[j] = xv * half_bits_to_float((uint16_t)(sw[j >> 1] >> (16 * (j & 1))));
+                }
+#pragma unroll
+                for (int st = 1; st < 8; st <<= 1)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        if (!(j & st)) {
+                            const float a = v[j], b = v[j | st];
+                            v[j] = a + b;
+                            v[j | st] = a - b;
+                        }
+                auto lane_stage = [&](auto sc) {
+                    constexpr int S = decltype(sc)::value;
+                    const float sgn = (pi & S) ? -1.f : 1.f;
+                    float pv[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) pv[j] = dpp_xor<S>(v[j]);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(v[j], sgn, pv[j]);
+                };
+                lane_stage(std::integral_constant<int, 1>{});
+                lane_stage(std::integral_constant<int, 2>{});
+                lane_stage(std::integral_constant<int, 4>{});
+                lane_stage(std::integral_constant<int, 8>{});
+                const int blk = (4 * q + g) * W + wave;
+                if (blk < nblk) {
+                    const int kbl = blk / rows, r = blk - kbl * rows;
+                    h8 hi, lo;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const float e = v[j] * 0.08838834764831844055f;
+                        hi[j] = (_Float16)e;
+                        lo[j] = (_Float16)(e - (float)hi[j]);
+                    }
+                    const int r4 = pi >> 3, kg = (pi >> 1) & 3, half = pi & 1;
+                    uint8_t *bp = frag + (size_t)((kbl * 2 + r4) * 2 + half) * blk_bytes;
+                    *(h8 *)(bp + ((kg * 2 + 0) * rows + r) * 16) = hi;
+                    *(h8 *)(bp + ((kg * 2 + 1) * rows + r) * 16) = lo;
+                }
             }
         }
     };
+    // at most one block per wave (rows 1 and short k): one block per wave with
+    // 2 elements per lane (stride 1 inside the lane, 2 .. 64 across all 64
+    // lanes) is faster than putting the blocks on 16-lane rows of fewer waves
+    auto prologue_one = [&](auto is_f16) {
+        constexpr bool XF16 = decltype(is_f16)::value;
+        const int blk = wave < nblk ? wave : nblk - 1;
+        const int kbl = blk / rows, r = blk - kbl * rows;
+        const int kb = kb0 + kbl;
+        const uint32_t ps = ((const uint32_t *)(records + (size_t)kb * GB + 2048 * K))[lane];  // su pair
+        const size_t xi = (size_t)r * x_stride + (size_t)kb * 128 + 2 * lane;
+        float a, b;
+        if constexpr (XF16) {
+            a = half_bits_to_float(((const uint16_t *)x)[xi]);
+            b = half_bits_to_float(((const uint16_t *)x)[xi + 1]);
+        } else {
+            a = ((const float *)x)[xi];
+            b = ((const float *)x)[xi + 1];
+        }
+        if (wave < nblk) {
+            a *= half_bits_to_float((uint16_t)(ps & 0xffffu));
+            b *= half_bits_to_float((uint16_t)(ps >> 16));
+            h128_pair(a, b, lane);
+            // elements 2 lane (+1): r4 = lane / 32, kg = lane / 8 % 4, half = lane / 4 % 2,
+            // position 2 (lane % 4) (+1) of the 16-byte slot
+            const _Float16 ha = (_Float16)a, hb = (_Float16)b;
+            const h2 hi = {ha, hb}, lo = {(_Float16)(a - (float)ha), (_Float16)(b - (float)hb)};
+            const int r4 = lane >> 5, kg = (lane >> 3) & 3, half = (lane >> 2) & 1, jj = 2 * (lane & 3);
+            uint8_t *bp = frag + (size_t)((kbl * 2 + r4) * 2 + half) * blk_bytes + jj * 2;
+            *(h2 *)(bp + ((kg * 2 + 0) * rows + r) * 16) = hi;
+            *(h2 *)(bp + ((kg * 2 + 1) * rows + r) * 16) = lo;
+        }
+    };
     auto prologue_x = [&](auto is_f16) {
-        const int nq = (nblk + W - 1) / W;  // slots of wave 0 (the most)
-        if (nq <= 1) prologue(std::integral_constant<int, 1>{}, is_f16);
+        const int nq = (nblk + 4 * W - 1) / (4 * W);  // units of wave 0 (the most)
+        if (nblk <= W) prologue_one(is_f16);
+        else if (nq <= 1) prologue(std::integral_constant<int, 1>{}, is_f16);
         else if (nq <= 2) prologue(std::integral_constant<int, 2>{}, is_f16);
-        else if (nq <= 4) prologue(std::integral_constant<int, 4>{}, is_f16);
-        else if (nq <= 8) prologue(std::integral_constant<int, 8>{}, is_f16);
-        else prologue(std::integral_constant<int, kGemvPrepMax>{}, is_f16);
+        else prologue(std::integral_constant<int, 4>{}, is_f16);
     };
     if (x_f16) prologue_x(std::true_type{});
     else prologue_x(std::false_type{});
