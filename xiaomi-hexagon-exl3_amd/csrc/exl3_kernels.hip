@@ -863,10 +863,38 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
         }
         if (!arrive_last(counters + nb, (unsigned)splits, &last_flag)) return;
         const float *all = partials + (size_t)nb * splits * (size_t)nval;
+        // each value summed in split order (the result does not depend on which
+        // workgroup arrived last); with two values per thread the loads of both
+        // are in flight together (one round trip instead of two)
+        auto sum_all = [&](auto nv_c) {
+            constexpr int NV = decltype(nv_c)::value, B = 16;
 #pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int t = tid + i * NT;
-            psum[i] = t < nval ? sum_splits(all + t, splits, (size_t)nval) : 0.f;
+            for (int i = 0; i < PER; ++i) psum[i] = 0.f;
+            for (int base = 0; base < splits; base += B) {
+                float v[NV][B];
+#pragma unroll
+                for (int i = 0; i < NV; ++i) {
+                    const int t = tid + i * NT;
+#pragma unroll
+                    for (int jb = 0; jb < B; ++jb) {
+                        const int sp = base + jb < splits ? base + jb : splits - 1;  // repeats are not added
+                        v[i][jb] = t < nval ? load_coherent(all + t + (size_t)sp * nval) : 0.f;
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < NV; ++i)
+#pragma unroll
+                    for (int jb = 0; jb < B; ++jb)
+                        if (base + jb < splits) psum[i] += v[i][jb];
+            }
+        };
+        static_assert(PER == 2, "two values per thread at most");
+        if (nval <= NT) {  // rows <= 4: one value per thread
+            const float q = tid < nval ? sum_splits(all + tid, splits, (size_t)nval) : 0.f;
+            psum[0] = q;
+            psum[1] = 0.f;
+        } else {
+            sum_all(std::integral_constant<int, 2>{});
         }
         if (tid == 0) reset_counter(counters + nb);  // self-reset for the next call
     }
