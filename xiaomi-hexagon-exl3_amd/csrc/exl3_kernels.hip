@@ -68,27 +68,6 @@ __device__ __forceinline__ void reset_counter(unsigned *counter) {
     __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// sum_{sp < splits} q[sp * stride] in ascending sp order.  Up to 16 coherent
-// loads are in flight before the first add (the addresses past `splits` repeat
-// the last valid one and are not added), so the exchange costs one L2 round
-// trip per 16 splits rather than one per load.
-__device__ __forceinline__ float sum_splits(const float *q, int splits, size_t stride) {
-    constexpr int B = 16;
-    float sum = 0.f;
-    for (int base = 0; base < splits; base += B) {
-        float v[B];
-#pragma unroll
-        for (int j = 0; j < B; ++j) {
-            const int sp = base + j < splits ? base + j : splits - 1;
-            v[j] = load_coherent(q + (size_t)sp * stride);
-        }
-#pragma unroll
-        for (int j = 0; j < B; ++j)
-            if (base + j < splits) sum += v[j];
-    }
-    return sum;
-}
-
 // Tile address of trellis tile (rk, cn) of a k x n matrix.
 template <int K>
 __device__ __forceinline__ const uint32_t *tile_ptr(const uint8_t *src, int records_layout, size_t k, size_t n,
@@ -854,61 +833,9 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
         }
         psum[i] = v;
     }
-    if (splits > 1) {
-        float *mine = partials + ((size_t)nb * splits + s) * (size_t)nval;
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int t = tid + i * NT;
-            if (t < nval) store_coherent(mine + t, psum[i]);
-        }
-        if (!arrive_last(counters + nb, (unsigned)splits, &last_flag)) return;
-        const float *all = partials + (size_t)nb * splits * (size_t)nval;
-        // each value summed in split order (the result does not depend on which
-        // workgroup arrived last); with two values per thread the loads of both
-        // are in flight together (one round trip instead of two)
-        auto sum_all = [&](auto nv_c) {
-            constexpr int NV = decltype(nv_c)::value, B = 16;
-#pragma unroll
-            for (int i = 0; i < PER; ++i) psum[i] = 0.f;
-            for (int base = 0; base < splits; base += B) {
-                float v[NV][B];
-#pragma unroll
-                for (int i = 0; i < NV; ++i) {
-                    const int t = tid + i * NT;
-#pragma unroll
-                    for (int jb = 0; jb < B; ++jb) {
-                        const int sp = base + jb < splits ? base + jb : splits - 1;  // repeats are not added
-                        v[i][jb] = t < nval ? load_coherent(all + t + (size_t)sp * nval) : 0.f;
-                    }
-                }
-#pragma unroll
-                for (int i = 0; i < NV; ++i)
-#pragma unroll
-                    for (int jb = 0; jb < B; ++jb)
-                        if (base + jb < splits) psum[i] += v[i][jb];
-            }
-        };
-        static_assert(PER == 2, "two values per thread at most");
-        if (nval <= NT) {  // rows <= 4: one value per thread
-            const float q = tid < nval ? sum_splits(all + tid, splits, (size_t)nval) : 0.f;
-            psum[0] = q;
-            psum[1] = 0.f;
-        } else {
-            sum_all(std::integral_constant<int, 2>{});
-        }
-        if (tid == 0) reset_counter(counters + nb);  // self-reset for the next call
-    }
-    // 6. output H128 per row (one wave per row, registers) and sv
-    float *ybuf = red + P * nval;
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const int t = tid + i * NT;
-        if (t < nval) ybuf[t] = psum[i];
-    }
-    __syncthreads();
-    for (int rr = wave; rr < rows; rr += W) {
-        float a0 = ybuf[rr * 128 + lane], a1 = ybuf[rr * 128 + lane + 64];
+    // output of row rr from its sums a0 (element lane) and a1 (lane + 64): H128
+    // over the 128 columns, sv (src/exl3-ggml.cpp:84-90), the optional residual
+    auto finish_row = [&](int rr, float a0, float a1) {
         h128_wave(a0, a1, lane);
         a0 *= sv0;
         a1 *= sv1;
@@ -930,7 +857,54 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
             ((float *)y)[o + lane] = a0;
             ((float *)y)[o + lane + 64] = a1;
         }
+    };
+    if (splits > 1) {
+        float *mine = partials + ((size_t)nb * splits + s) * (size_t)nval;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int t = tid + i * NT;
+            if (t < nval) store_coherent(mine + t, psum[i]);
+        }
+        if (!arrive_last(counters + nb, (unsigned)splits, &last_flag)) return;
+        // the last workgroup: wave r sums row r's elements lane and lane + 64 over
+        // the splits in split order (so the result does not depend on which
+        // workgroup arrived last), all of a lane's loads in flight together,
+        // straight into the registers of the output transform
+        const float *all = partials + (size_t)nb * splits * (size_t)nval;
+        for (int rr = wave; rr < rows; rr += W) {
+            constexpr int B = 16;
+            float a0 = 0.f, a1 = 0.f;
+            for (int base = 0; base < splits; base += B) {
+                float v0[B], v1[B];
+#pragma unroll
+                for (int jb = 0; jb < B; ++jb) {
+                    const int sp = base + jb < splits ? base + jb : splits - 1;  // repeats are not added
+                    const float *q = all + (size_t)sp * nval + rr * 128 + lane;
+                    v0[jb] = load_coherent(q);
+                    v1[jb] = load_coherent(q + 64);
+                }
+#pragma unroll
+                for (int jb = 0; jb < B; ++jb)
+                    if (base + jb < splits) {
+                        a0 += v0[jb];
+                        a1 += v1[jb];
+                    }
+            }
+            finish_row(rr, a0, a1);
+        }
+        if (tid == 0) reset_counter(counters + nb);  // self-reset for the next call
+        return;
     }
+    // 6. (one workgroup per column group) output H128 per row from the LDS sums
+    float *ybuf = red + P * nval;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int t = tid + i * NT;
+        if (t < nval) ybuf[t] = psum[i];
+    }
+    __syncthreads();
+    for (int rr = wave; rr < rows; rr += W) finish_row(rr, ybuf[rr * 128 + lane], ybuf[rr * 128 + lane + 64]);
 }
 
 // LDS bytes of a GEMV workgroup: its B fragments, reused after the main loop for
