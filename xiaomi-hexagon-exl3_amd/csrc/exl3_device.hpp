@@ -211,36 +211,43 @@ __device__ __forceinline__ float dpp_xor(float v) {
 // l + 64 in v1.  Stages 1..32 pair lanes l and l ^ step, stage 64 pairs v0/v1;
 // each butterfly is (a + b, a - b) with a the lower index, in the reference's
 // stage order (src/exl3_codec.cpp:153-165), then the 1/sqrt(128) scale.  Lane
-// exchanges use DPP (xor 1..8 inside 16-lane rows), ds_swizzle (xor 16) and
-// ds_bpermute (xor 32); each butterfly is one fma with a +-1 lane sign, exact
-// like a +- b.
-template <int STEP>
-__device__ __forceinline__ float lane_xor(float v, int bperm_addr32) {
-    if constexpr (STEP == 32) {
-        return __int_as_float(__builtin_amdgcn_ds_bpermute(bperm_addr32, __float_as_int(v)));
-    } else if constexpr (STEP == 16) {
-        return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (STEP << 10)));
+// exchanges are VALU only: DPP for xor 1..8 inside 16-lane rows, gfx950's
+// v_permlane16_swap / v_permlane32_swap for xor 16 / 32; each butterfly is one
+// fma with a +-1 lane sign, exact like a +- b.
+//
+// permlane{16,32}_swap(v, v) returns r0 = v with every upper half (odd 16-lane
+// row, or lanes 32..63) replaced by the lower half next to it and r1 = v with
+// every lower half replaced by the upper one: a lower lane reads own = r0,
+// partner = r1, an upper lane partner = r0, own = r1, so r0 + sgn r1 is the
+// butterfly on both.
+template <int S>
+__device__ __forceinline__ float lane_butterfly(float v, int lane) {
+    const float sgn = (lane & S) ? -1.f : 1.f;  // upper element: partner - own
+    if constexpr (S == 16 || S == 32) {
+        const int iv = __float_as_int(v);
+        const auto r = [&] {
+            if constexpr (S == 16) return __builtin_amdgcn_permlane16_swap(iv, iv, false, false);
+            else return __builtin_amdgcn_permlane32_swap(iv, iv, false, false);
+        }();
+        return __builtin_fmaf(__int_as_float(r[1]), sgn, __int_as_float(r[0]));
     } else {
-        return dpp_xor<STEP>(v);  // VALU, no LDS round trip
+        return __builtin_fmaf(v, sgn, dpp_xor<S>(v));
     }
 }
 
 template <int STEP>
-__device__ __forceinline__ void h128_stage(float &v0, float &v1, int lane, int bperm_addr32) {
-    const float sgn = (lane & STEP) ? -1.f : 1.f;  // upper element: partner - own
-    const float p0 = lane_xor<STEP>(v0, bperm_addr32), p1 = lane_xor<STEP>(v1, bperm_addr32);
-    v0 = __builtin_fmaf(v0, sgn, p0);
-    v1 = __builtin_fmaf(v1, sgn, p1);
+__device__ __forceinline__ void h128_stage(float &v0, float &v1, int lane) {
+    v0 = lane_butterfly<STEP>(v0, lane);
+    v1 = lane_butterfly<STEP>(v1, lane);
 }
 
 __device__ __forceinline__ void h128_wave(float &v0, float &v1, int lane) {
-    const int addr32 = (lane ^ 32) << 2;
-    h128_stage<1>(v0, v1, lane, addr32);
-    h128_stage<2>(v0, v1, lane, addr32);
-    h128_stage<4>(v0, v1, lane, addr32);
-    h128_stage<8>(v0, v1, lane, addr32);
-    h128_stage<16>(v0, v1, lane, addr32);
-    h128_stage<32>(v0, v1, lane, addr32);
+    h128_stage<1>(v0, v1, lane);
+    h128_stage<2>(v0, v1, lane);
+    h128_stage<4>(v0, v1, lane);
+    h128_stage<8>(v0, v1, lane);
+    h128_stage<16>(v0, v1, lane);
+    h128_stage<32>(v0, v1, lane);
     const float a = v0, b = v1;
     v0 = (a + b) * 0.08838834764831844055f;
     v1 = (a - b) * 0.08838834764831844055f;
@@ -249,16 +256,15 @@ __device__ __forceinline__ void h128_wave(float &v0, float &v1, int lane) {
 // The same transform with lane l owning elements 2 l (e0) and 2 l + 1 (e1): the
 // stride-1 butterfly is inside the lane, strides 2..64 pair lanes l and l ^ 1..32.
 __device__ __forceinline__ void h128_pair(float &e0, float &e1, int lane) {
-    const int addr32 = (lane ^ 32) << 2;
     const float a = e0, b = e1;
     e0 = a + b;
     e1 = a - b;
-    h128_stage<1>(e0, e1, lane, addr32);
-    h128_stage<2>(e0, e1, lane, addr32);
-    h128_stage<4>(e0, e1, lane, addr32);
-    h128_stage<8>(e0, e1, lane, addr32);
-    h128_stage<16>(e0, e1, lane, addr32);
-    h128_stage<32>(e0, e1, lane, addr32);
+    h128_stage<1>(e0, e1, lane);
+    h128_stage<2>(e0, e1, lane);
+    h128_stage<4>(e0, e1, lane);
+    h128_stage<8>(e0, e1, lane);
+    h128_stage<16>(e0, e1, lane);
+    h128_stage<32>(e0, e1, lane);
     e0 *= 0.08838834764831844055f;
     e1 *= 0.08838834764831844055f;
 }

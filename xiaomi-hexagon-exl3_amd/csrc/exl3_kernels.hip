@@ -1130,7 +1130,8 @@ __device__ __forceinline__ int gemm_w_offset(int n, int chunk) {  // halves
 // Output of accumulator values in the 32x32 MFMA D layout: t[cb][i] is column
 // 32 cb + lane % 32 of row row0 + (i % 4) + 8 (i / 4) + 4 (lane / 32).  H128 over
 // the 128 columns of each row in natural stage order (strides 1..16 pair lanes
-// lane ^ 1..16, strides 32 and 64 pair blocks cb ^ 1, 2; src/exl3_codec.cpp:153-165),
+// lane ^ 1..16 by DPP and v_permlane16_swap, strides 32 and 64 pair blocks cb ^ 1, 2;
+// src/exl3_codec.cpp:153-165),
 // then 1/sqrt(128) and sv (src/exl3-ggml.cpp:84-90).
 template <int NE>
 __device__ __forceinline__ void gemm_rows_out(float (&t)[4][NE], int lane, int row0, const uint16_t *svp, int rows,
@@ -1141,16 +1142,23 @@ __device__ __forceinline__ void gemm_rows_out(float (&t)[4][NE], int lane, int r
     // and butterflies of one stage issue back to back without wait states
     auto lane_stage = [&](auto sc) {
         constexpr int S = decltype(sc)::value;
-        const float sgn = (l32 & S) ? -1.f : 1.f;
-        float p[4][NE];
+        if constexpr (S == 16) {  // v_permlane16_swap (lane_butterfly): VALU, no LDS round trip
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb)
+            for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-            for (int i = 0; i < NE; ++i) p[cb][i] = lane_xor<S>(t[cb][i], 0);
+                for (int i = 0; i < NE; ++i) t[cb][i] = lane_butterfly<16>(t[cb][i], l32);
+        } else {
+            const float sgn = (l32 & S) ? -1.f : 1.f;
+            float p[4][NE];
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb)
+            for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-            for (int i = 0; i < NE; ++i) t[cb][i] = __builtin_fmaf(t[cb][i], sgn, p[cb][i]);
+                for (int i = 0; i < NE; ++i) p[cb][i] = dpp_xor<S>(t[cb][i]);
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+                for (int i = 0; i < NE; ++i) t[cb][i] = __builtin_fmaf(t[cb][i], sgn, p[cb][i]);
+        }
     };
     lane_stage(std::integral_constant<int, 1>{});
     lane_stage(std::integral_constant<int, 2>{});
