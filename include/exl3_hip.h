@@ -10,8 +10,10 @@
  *   exl3_hip_mul_mat      <- ggml_exl3_mul_mat        src/exl3-ggml.cpp:51-92,
  *                            declared include/exl3-block.h:46, dispatched from
  *                            ggml_compute_forward_mul_mat (patches/llama-exl3.patch:44-51);
- *                            device twin op_exl3_matmul src/exl3-htp.c:159-232;
- *                            scalar model exl3_iface_matmul src/hexagon/exl3_iface.idl:13-15
+ *                            device twin op_exl3_matmul src/exl3-htp.c:159-232
+ *   exl3_hip_iface_matmul <- exl3_iface_matmul src/hexagon/exl3_service.c:265-305
+ *                            (IDL src/hexagon/exl3_iface.idl:13-15): the same layer on the
+ *                            upstream tile layout with separate su / sv, fp32 in and out
  *   exl3_hip_decode       <- exl3::decode_inner(_slice) src/exl3_codec.cpp:123-145
  *                            (and exl3_iface_decode src/hexagon/exl3_iface.idl:5-7)
  *   exl3_hip_reconstruct  <- exl3::reconstruct(_slice)  src/exl3_codec.cpp:169-204
@@ -191,6 +193,27 @@ exl3_status exl3_hip_hadamard128(float *values, size_t count, hipStream_t stream
 /* Upstream tiles [k/16][n/16][16*bits] + su[k] + sv[n] -> records. */
 exl3_status exl3_hip_pack_records(const uint16_t *packed, const uint16_t *su, const uint16_t *sv,
                                   unsigned bits, size_t k, size_t n, void *records, hipStream_t stream);
+
+/* The DSP service's layer exl3_iface_matmul (src/hexagon/exl3_service.c:265-305,
+ * IDL src/hexagon/exl3_iface.idl:13-15): y = x . diag(su) H W_hat H diag(sv) on the
+ * upstream tile layout with separate su / sv vectors, fp32 in and out.  One call packs
+ * the tiles and scales into group records inside the workspace (exl3_hip_pack_records)
+ * and runs exl3_hip_mul_mat on them, so the weights are decoded once per call, as the
+ * service decodes them; callers that reuse the weights pack once and call
+ * exl3_hip_mul_mat instead.
+ *   packed      device, [k/16][n/16][16*bits] u16 = k*n*bits/8 bytes, 16-byte aligned
+ *   suh, svh    device fp16 su[k] and sv[n], 16-byte aligned
+ *   x, y        device fp32, batch x k and batch x n, dense rows (the service's layout)
+ *   workspace   >= exl3_hip_iface_matmul_workspace_bytes(bits, k, n, batch), 256-byte
+ *               aligned, zero-filled before first use; NULL -> an internal one
+ * The service also caps batch at 8 and k*n at 64 Mi (its memory); here batch is any row
+ * count exl3_hip_mul_mat accepts.  Rejections follow the service: bits 1..8, codebook
+ * 0..2, k and n nonzero multiples of 128, batch >= 1 (EXL3_INVAL_PARAMS where the
+ * service returns 2). */
+size_t exl3_hip_iface_matmul_workspace_bytes(unsigned bits, size_t k, size_t n, size_t batch);
+exl3_status exl3_hip_iface_matmul(unsigned bits, unsigned codebook, size_t k, size_t n, size_t batch,
+                                  const uint16_t *packed, const uint16_t *suh, const uint16_t *svh, const float *x,
+                                  float *y, void *workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* *result (device int) = 1 when every su/sv value of every record is finite,
  * 0 otherwise; EXL3_INVAL_PARAMS when nbytes is not a whole number of records. */

@@ -512,3 +512,46 @@ int orc_mul_mat(const void *records, unsigned bits, unsigned cb, size_t k, size_
     return orc_mul_mat_groups(records, bits, cb, k, n, x, x_is_f16, rows, x_stride_bytes, y,
                               y_stride_bytes, nthreads, 0, n / 128);
 }
+
+/* ------------------------------------------------ DSP service layer */
+
+/* src/hexagon/exl3_service.c:265-305 (exl3_iface_matmul): xh[b] = H128(x[b] * su) (:280-286),
+ * result[b][16 cn + col] += xh[b][16 rk + row] * W[16 rk + row][16 cn + col] in
+ * binary32, loop order rk -> cn -> row -> col -> b (:248-261, tiles decoded by the
+ * codec's formula, :67-86), then y[b] = H128(result[b]) * sv (:297-300). */
+int orc_iface_matmul(unsigned bits, unsigned cb, size_t k, size_t n, size_t batch, const uint16_t *packed,
+                     const uint16_t *suh, const uint16_t *svh, const float *x, float *y)
+{
+    if (!valid_rate(bits, cb) || !valid_shape(k, n, 128) || !batch || batch > 8 ||
+        (uint64_t)k * n > 64u * 1024u * 1024u)
+        return ORC_EINVAL;
+    const uint16_t *table = codebook_table(cb);
+    float *xh = (float *)malloc(batch * k * sizeof(float));
+    float *result = (float *)calloc(batch * n, sizeof(float));
+    if (!xh || !result) {
+        free(xh);
+        free(result);
+        return ORC_EINVAL;
+    }
+    for (size_t b = 0; b < batch; ++b) {
+        for (size_t i = 0; i < k; ++i) xh[b * k + i] = x[b * k + i] * orc_half_to_float(suh[i]);
+        for (size_t blk = 0; blk < k; blk += 128) h128_block(xh + b * k + blk);
+    }
+    uint16_t tile[256];
+    for (size_t rk = 0; rk < k / 16; ++rk)
+        for (size_t cn = 0; cn < n / 16; ++cn) {
+            decode_tile_unchecked(packed + (rk * (n / 16) + cn) * 16u * bits, bits, table, tile, 16);
+            for (size_t row = 0; row < 16; ++row)
+                for (size_t col = 0; col < 16; ++col) {
+                    const float w = orc_half_to_float(tile[row * 16 + col]);
+                    for (size_t b = 0; b < batch; ++b) result[b * n + cn * 16 + col] += xh[b * k + rk * 16 + row] * w;
+                }
+        }
+    for (size_t b = 0; b < batch; ++b) {
+        for (size_t blk = 0; blk < n; blk += 128) h128_block(result + b * n + blk);
+        for (size_t i = 0; i < n; ++i) y[b * n + i] = result[b * n + i] * orc_half_to_float(svh[i]);
+    }
+    free(xh);
+    free(result);
+    return ORC_OK;
+}

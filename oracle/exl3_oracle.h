@@ -94,6 +94,14 @@ int orc_mul_mat_groups(const void *records, unsigned bits, unsigned cb, size_t k
                        float *y, size_t y_stride_bytes, unsigned nthreads, size_t nb_begin,
                        size_t nb_end);
 
+/* The DSP service's layer exl3_iface_matmul, src/hexagon/exl3_service.c:265-305:
+ * the same math as orc_mul_mat on the upstream tile layout [k/16][n/16][16 bits]
+ * with separate su[k] / sv[n] (fp16), fp32 x (batch x k) and y (batch x n),
+ * accumulated in the service's loop order rk -> cn -> row -> col -> b (:248-261).
+ * Argument checks of :270-273 (batch <= 8, k * n <= 64 Mi) -> ORC_EINVAL. */
+int orc_iface_matmul(unsigned bits, unsigned cb, size_t k, size_t n, size_t batch, const uint16_t *packed,
+                     const uint16_t *suh, const uint16_t *svh, const float *x, float *y);
+
 #ifdef __cplusplus
 }
 #endif

@@ -48,6 +48,8 @@ class Oracle:
                                          ctypes.c_int, _sz, _sz, _f32p, _sz, ctypes.c_uint, _sz, _sz]
         L.orc_get_rows.argtypes = [ctypes.c_void_p, ctypes.c_uint, ctypes.c_uint, _sz, _sz, ctypes.c_void_p, _sz,
                                    _f32p, _sz]
+        L.orc_iface_matmul.argtypes = [ctypes.c_uint, ctypes.c_uint, _sz, _sz, _sz, _u16p, _u16p, _u16p, _f32p,
+                                       _f32p]
         self.L = L
 
     def codebook_table(self, cb):
@@ -133,6 +135,19 @@ class Oracle:
         if rc:
             raise ValueError("mul_mat rejected its arguments")
         return y
+
+    def iface_matmul(self, packed, su, sv, bits, cb, k, n, x):
+        """The DSP service's layer: upstream tiles + separate su/sv, x [batch, k] fp32 -> y [batch, n] fp32"""
+        p = np.ascontiguousarray(packed, dtype=np.uint16)
+        su = np.ascontiguousarray(su).view(np.uint16)
+        sv = np.ascontiguousarray(sv).view(np.uint16)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.zeros((x.shape[0], n), dtype=np.float32)
+        if self.L.orc_iface_matmul(bits, cb, k, n, x.shape[0], _ptr(p, _u16p), _ptr(su, _u16p), _ptr(sv, _u16p),
+                                   _ptr(x, _f32p), _ptr(y, _f32p)):
+            raise ValueError("iface_matmul rejected its arguments")
+        return y
+
 
 
 class Reference:

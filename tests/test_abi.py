@@ -86,6 +86,20 @@ def test_host_side_status_and_planning():
     bad = (ctypes.c_size_t * 5)(0x10000, 16, 24, 0x20000, 4)        # n not a multiple of 16
     assert L.exl3_hip_decode_batch(ctypes.cast(bad, ctypes.c_void_p), 1, 0, 2, None) == 1
     assert L.exl3_hip_status_string(3) == b"workspace too small"
+    # the DSP service's layer on upstream tiles: its argument checks, then workspace sizing
+    assert L.exl3_hip_iface_matmul(4, 2, 128, 128, 1, None, None, None, None, None, None, 0, None) == 1  # NULLs
+    for bits, cb, k, n, batch in ((0, 2, 128, 128, 1), (9, 2, 128, 128, 1), (4, 3, 128, 128, 1),
+                                  (4, 2, 100, 128, 1), (4, 2, 128, 96, 1), (4, 2, 128, 128, 0)):
+        assert L.exl3_hip_iface_matmul(bits, cb, k, n, batch, 0x10000, 0x20000, 0x30000, 0x40000, 0x50000,
+                                       None, 0, None) == 1, (bits, cb, k, n, batch)
+        if cb <= 2:  # the workspace size does not depend on the codebook
+            assert L.exl3_hip_iface_matmul_workspace_bytes(bits, k, n, batch) == 0
+    assert L.exl3_hip_iface_matmul(4, 2, 128, 128, 1, 0x10008, 0x20000, 0x30000, 0x40000, 0x50000,
+                                   None, 0, None) == 1   # packed not 16-byte aligned
+    ws = L.exl3_hip_iface_matmul_workspace_bytes(4, 14336, 4096, 8)
+    assert ws >= L.exl3_hip_mul_mat_workspace_bytes(14336, 4096, 8) + 3584 * (2048 * 4 + 512)
+    assert L.exl3_hip_iface_matmul(4, 2, 14336, 4096, 8, 0x10000, 0x20000, 0x30000, 0x40000, 0x50000,
+                                   0x100000, ws - 1, None) == 3   # caller workspace too small
 
 
 @pytest.mark.skipif(not (ROOT / "oracle" / "_ref" / "check_ref").exists(), reason="reference build absent")

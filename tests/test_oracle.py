@@ -298,16 +298,71 @@ def test_layer_thread_partition_bit_identical(oracle):
     assert np.array_equal(ys[:, 128:384], y1[:, 128:384])
 
 
-def test_planted_mistakes_fail_the_gate(oracle):
-    """The NMSE gate used for the layer catches plausible slips in the formula."""
-    d = np.load(GOLD / "layer.npz", allow_pickle=False)
-    k, n, bits, cb, rows = (int(v) for v in d["meta"])
-    rec, x, y_ref = d["records"], d["x"], d["y_from_reconstruct"]
+def upstream_from_records(rec, k, n, bits):
+    """Records (u16 view) -> upstream tiles [k/16, n/16, 16 bits], su [k], sv [n] (the inverse of the
+    record assembly of tools/export_native_gguf.py:27-36)."""
     recs = rec.reshape(n // 128, k // 128, -1)
     tiles = recs[:, :, : 1024 * bits]
     p = tiles.reshape(n // 128, k // 128, 8, 8, 16 * bits).transpose(1, 2, 0, 3, 4).reshape(k // 16, n // 16, 16 * bits)
     su = recs[0, :, 1024 * bits: 1024 * bits + 128].reshape(-1).view(np.float16)
     sv = recs[:, 0, 1024 * bits + 128:].reshape(-1).view(np.float16)
+    return np.ascontiguousarray(p), np.ascontiguousarray(su), np.ascontiguousarray(sv)
+
+
+def test_iface_matmul_layer_golden(oracle):
+    """The DSP service's layer (src/hexagon/exl3_service.c:265-305: upstream tiles, separate su/sv,
+    fp32 in and out) on the layer fixture, whose records carry the same tiles and scales."""
+    d = np.load(GOLD / "layer.npz", allow_pickle=False)
+    k, n, bits, cb, rows = (int(v) for v in d["meta"])
+    p, su, sv = upstream_from_records(d["records"], k, n, bits)
+    y = oracle.iface_matmul(p, su, sv, bits, cb, k, n, d["x"].astype(np.float32))
+    assert nmse(y, d["y"]) < 1e-10
+    assert nmse(y, d["y_from_reconstruct"]) < 1e-5   # tests/test-exl3-graph.cpp:100-104 gate
+
+
+@pytest.mark.parametrize("bits,cb", [(1, 2), (3, 0), (5, 1), (8, 2)])
+def test_iface_matmul_vs_float64_and_ggml_layer(oracle, bits, cb):
+    k, n, rows = 384, 256, 8
+    p = synth.packed_tiles(bits * 17 + cb, k, n, bits)
+    su, sv = synth.layer_scales(bits + 40, k, n)
+    x = synth.activations(bits + 50, rows, k).astype(np.float32)
+    y = oracle.iface_matmul(p, su, sv, bits, cb, k, n, x)
+    assert nmse(y, layer64(oracle.decode_inner(p, k, n, bits, cb), su, sv, x)) < 1e-10
+    # the ggml op on the records of the same weights: same math, another fp32 summation order
+    y_ggml = oracle.mul_mat(synth.pack_records(p, su, sv, bits), bits, cb, k, n, x)
+    assert nmse(y, y_ggml) < 1e-11
+    # a wrong tile order (column-major tile grid) or swapped scale vectors fail the float64 check
+    p_t = np.ascontiguousarray(p.reshape(k // 16, n // 16, -1).transpose(1, 0, 2)).reshape(k // 16, n // 16, -1)
+    assert nmse(oracle.iface_matmul(p_t, su, sv, bits, cb, k, n, x), y) > 1e-3
+    assert nmse(oracle.iface_matmul(p, su[::-1].copy(), sv, bits, cb, k, n, x), y) > 1e-3
+
+
+def test_iface_matmul_rejects(oracle):
+    """The service's argument checks (src/hexagon/exl3_service.c:270-273)."""
+    p = np.zeros(16, dtype=np.uint16)
+    s = np.zeros(128, dtype=np.float16)
+
+    def rejects(bits, cb, k, n, batch):
+        with pytest.raises(ValueError):
+            oracle.iface_matmul(p, s, s, bits, cb, k, n, np.zeros((batch, k), dtype=np.float32))
+
+    rejects(0, 2, 128, 128, 1)
+    rejects(9, 2, 128, 128, 1)
+    rejects(4, 3, 128, 128, 1)
+    rejects(4, 2, 100, 128, 1)
+    rejects(4, 2, 128, 96, 1)
+    rejects(4, 2, 128, 128, 9)        # batch above 8
+    rejects(4, 2, 8192, 8320, 1)      # k * n above 64 Mi
+    with pytest.raises(ValueError):
+        oracle.iface_matmul(p, s, s, 4, 2, 128, 128, np.zeros((0, 128), dtype=np.float32))
+
+
+def test_planted_mistakes_fail_the_gate(oracle):
+    """The NMSE gate used for the layer catches plausible slips in the formula."""
+    d = np.load(GOLD / "layer.npz", allow_pickle=False)
+    k, n, bits, cb, rows = (int(v) for v in d["meta"])
+    rec, x, y_ref = d["records"], d["x"], d["y_from_reconstruct"]
+    p, su, sv = upstream_from_records(rec, k, n, bits)
     inner = oracle.decode_inner(p, k, n, bits, cb)
     good = layer64(inner, su, sv, x)
     assert nmse(good, y_ref) < 1e-5

@@ -315,6 +315,43 @@ exl3_status exl3_hip_pack_records(const uint16_t *packed, const uint16_t *su, co
     return from_hip(exl3k::launch_pack_records(packed, su, sv, (int)bits, k, n, records, stream));
 }
 
+// Workspace of exl3_hip_iface_matmul: the mul_mat workspace (its counters first,
+// so one zero-fill covers both), then the packed records.
+static size_t iface_records_offset(size_t k, size_t n, size_t batch) {
+    return (exl3_hip_mul_mat_workspace_bytes(k, n, batch) + 255) & ~(size_t)255;
+}
+
+size_t exl3_hip_iface_matmul_workspace_bytes(unsigned bits, size_t k, size_t n, size_t batch) {
+    if (bits < 1 || bits > 8 || !valid_matrix(k, n, 128) || batch < 1 || batch > kMaxRows) return 0;
+    return iface_records_offset(k, n, batch) + (n / 128) * (k / 128) * ((size_t)2048 * bits + 512);
+}
+
+// exl3_iface_matmul (src/hexagon/exl3_service.c:265-305): the argument checks of
+// its first statement (minus the service's memory caps), then the layer.
+exl3_status exl3_hip_iface_matmul(unsigned bits, unsigned codebook, size_t k, size_t n, size_t batch,
+                                  const uint16_t *packed, const uint16_t *suh, const uint16_t *svh, const float *x,
+                                  float *y, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (!valid_rate(bits, codebook) || !valid_matrix(k, n, 128) || batch < 1 || batch > kMaxRows)
+        return EXL3_INVAL_PARAMS;
+    if (!packed || !suh || !svh || !x || !y) return EXL3_INVAL_PARAMS;
+    if (!aligned(packed, 16) || !aligned(suh, 16) || !aligned(svh, 16) || !aligned(x, 4) || !aligned(y, 4))
+        return EXL3_INVAL_PARAMS;
+    const size_t need = exl3_hip_iface_matmul_workspace_bytes(bits, k, n, batch);
+    if (workspace) {
+        if (!aligned(workspace, 256)) return EXL3_INVAL_PARAMS;
+        if (workspace_bytes < need) return EXL3_WORKSPACE_TOO_SMALL;
+    } else {
+        const exl3_status st = internal_workspace(need, n, stream, &workspace);
+        if (st != EXL3_OK) return st;
+    }
+    const size_t roff = iface_records_offset(k, n, batch);
+    void *records = (uint8_t *)workspace + roff;
+    exl3_status st = exl3_hip_pack_records(packed, suh, svh, bits, k, n, records, stream);
+    if (st != EXL3_OK) return st;
+    return exl3_hip_mul_mat(records, bits, codebook, k, n, x, EXL3_F32, batch, k, y, EXL3_F32, n, workspace, roff,
+                            stream);
+}
+
 exl3_status exl3_hip_validate_records(const void *records, size_t nbytes, unsigned bits, int *result,
                                       hipStream_t stream) {
     if (bits < 1 || bits > 8 || !result || (nbytes && !records)) return EXL3_INVAL_PARAMS;

@@ -24,7 +24,7 @@ EXPORTS = [
     "exl3_hip_model_open", "exl3_hip_model_close", "exl3_hip_model_tensor_count", "exl3_hip_model_payload_bytes",
     "exl3_hip_model_hidden_size", "exl3_hip_model_vocab_size", "exl3_hip_model_bits_per_weight",
     "exl3_hip_model_embedding", "exl3_hip_model_matrix_count", "exl3_hip_model_matrix", "exl3_hip_model_record_bytes",
-    "exl3_hip_model_upload_records",
+    "exl3_hip_model_upload_records", "exl3_hip_iface_matmul_workspace_bytes", "exl3_hip_iface_matmul",
 ]
 
 
@@ -91,6 +91,10 @@ def load(path=LIB_PATH):
     L.exl3_hip_pack_records.argtypes = [vp, vp, vp, u, sz, sz, vp, st]
     L.exl3_hip_validate_records.restype = i
     L.exl3_hip_validate_records.argtypes = [vp, sz, u, vp, st]
+    L.exl3_hip_iface_matmul_workspace_bytes.restype = sz
+    L.exl3_hip_iface_matmul_workspace_bytes.argtypes = [u, sz, sz, sz]
+    L.exl3_hip_iface_matmul.restype = i
+    L.exl3_hip_iface_matmul.argtypes = [u, u, sz, sz, sz, vp, vp, vp, vp, vp, vp, sz, st]
     return L
 
 
@@ -328,6 +332,30 @@ def pack_records(packed, su, sv, bits, k, n, out=None, stream=None):
     _check(lib().exl3_hip_pack_records(_ptr(packed), _ptr(su), _ptr(sv), bits, k, n, _ptr(out), _stream(stream)),
            "pack_records")
     return out
+
+
+def iface_matmul(packed, suh, svh, x, bits, k, n, codebook=CB_MUL1, y=None, workspace=None, stream=None):
+    """The DSP service's layer (exl3_iface_matmul): upstream tiles [k/16, n/16, 16 bits] int16/uint16,
+    su [k] and sv [n] fp16, x [batch, k] fp32 (dense) -> y [batch, n] fp32, in one call."""
+    import torch
+    assert x.dim() == 2 and x.dtype == torch.float32 and x.is_contiguous() and x.shape[1] == k
+    if y is None:
+        y = torch.empty((x.shape[0], n), dtype=torch.float32, device=x.device)
+    assert y.dtype == torch.float32 and y.is_contiguous() and tuple(y.shape) == (x.shape[0], n)
+    wb = workspace.numel() if workspace is not None else 0
+    _check(lib().exl3_hip_iface_matmul(bits, codebook, k, n, x.shape[0], _ptr(packed), _ptr(suh), _ptr(svh), _ptr(x),
+                                       _ptr(y), _ptr(workspace), wb, _stream(stream)), "iface_matmul")
+    return y
+
+
+def new_iface_workspace(bits, k, n, batch, device="cuda"):
+    import torch
+    nbytes = lib().exl3_hip_iface_matmul_workspace_bytes(bits, k, n, batch)
+    if not nbytes:
+        raise Exl3Error(INVAL_PARAMS, "iface_matmul_workspace_bytes")
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    _check(lib().exl3_hip_workspace_init(_ptr(ws), nbytes, _stream()), "workspace_init")
+    return ws
 
 
 def validate_records(records, bits, stream=None):
