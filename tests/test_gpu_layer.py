@@ -62,9 +62,10 @@ def test_all_rates_and_codebooks(amd, oracle, bits):
             assert_layer_close(run(amd, rd, bits, k, n, x, cb), ref, what=f"bits={bits} cb={cb} rows={rows}")
 
 
-@pytest.mark.parametrize("rows", [1, 2, 4, 8])
+@pytest.mark.parametrize("rows", [1, 2, 4, 8, 9, 12, 16])
 def test_c3_full_size_gemv(amd, oracle, rows):
-    """4096 x 14336 at 4 bits (k=14336 in, n=4096 out), ragged decode batches"""
+    """4096 x 14336 at 4 bits (k=14336 in, n=4096 out), ragged decode batches up to the
+    GEMV's 16 rows (rows 9..16 use its second block of MFMA columns)"""
     k, n, bits = 14336, 4096, 4
     rec = make_layer(303, k, n, bits)
     x = synth.activations(304 + rows, rows, k)
@@ -74,7 +75,7 @@ def test_c3_full_size_gemv(amd, oracle, rows):
     assert rl < 1e-5  # hi/lo activation split keeps the GEMV at fp32-level accuracy
 
 
-@pytest.mark.parametrize("rows", [9, 32, 37, 128, 300])
+@pytest.mark.parametrize("rows", [17, 32, 37, 128, 300])
 def test_gemm_rows(amd, oracle, rows):
     k, n, bits = 1024, 384, 4
     rec = make_layer(400 + rows, k, n, bits)
@@ -123,7 +124,7 @@ def test_deterministic_and_workspaces(amd):
     import torch
     k, n, bits = 4096, 1024, 4
     rec = dev(make_layer(700, k, n, bits))
-    for rows in (1, 8, 64):
+    for rows in (1, 8, 13, 64):
         x = torch.from_numpy(synth.activations(701, rows, k)).cuda()
         y1 = amd.mul_mat(rec, bits, k, n, x).clone()
         y2 = amd.mul_mat(rec, bits, k, n, x).clone()
@@ -214,7 +215,7 @@ def test_one_workspace_serves_mixed_row_counts(amd):
     import torch
     k, n, bits = 2048, 4096, 4
     rd = dev(make_layer(820, k, n, bits))
-    seq = [300, 100, 300, 5, 300, 1, 37, 300, 8, 129]
+    seq = [300, 100, 300, 5, 300, 1, 37, 300, 8, 129, 16, 11, 300, 9]
     xs = {r: torch.from_numpy(synth.activations(821 + r, r, k)).cuda() for r in set(seq)}
     fresh = {}
     for r in set(seq):
@@ -230,11 +231,11 @@ def test_one_workspace_serves_mixed_row_counts(amd):
         assert torch.equal(y_internal, fresh[r]), f"internal workspace, call {i} rows={r}"
 
 
-@pytest.mark.parametrize("rows", [1, 3, 8, 12])
+@pytest.mark.parametrize("rows", [1, 3, 8, 12, 16, 20])
 def test_group_matches_single_layers(amd, oracle, rows):
     """q/k/v and gate/up of one decoder layer through exl3_hip_mul_mat_group: one launch
-    (rows <= 8) that serves several matrices sharing x; each output within the layer
-    tolerance of the oracle, and at rows > 8 (one call per matrix) equal to mul_mat"""
+    (rows <= 16, the GEMV) that serves several matrices sharing x; each output within the
+    layer tolerance of the oracle, and above (one call per matrix) equal to mul_mat"""
     import torch
     for k, shapes, bits in [(2048, [2048, 512, 512], 6), (2048, [6144, 6144], 4)]:
         recs = [make_layer(700 + i + bits, k, n, bits) for i, n in enumerate(shapes)]
@@ -244,7 +245,7 @@ def test_group_matches_single_layers(amd, oracle, rows):
         for i, (r, n) in enumerate(zip(recs, shapes)):
             y = ys[i].cpu().numpy()
             assert_layer_close(y, oracle.mul_mat(r, bits, 2, k, n, x), what=f"group {i} n={n} rows={rows}")
-            if rows > 8:
+            if rows > amd.lib().exl3_hip_gemv_max_rows():
                 single = amd.mul_mat(dev(r), bits, k, n, xd).cpu().numpy()
                 assert np.array_equal(y, single)
     L = amd.lib()

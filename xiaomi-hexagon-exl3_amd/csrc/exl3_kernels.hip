@@ -1,6 +1,6 @@
 // exl3_kernels.hip -- gfx950 kernels of the EXL3 packed-weight linear layer.
 //
-//   gemv_kernel      rows 1..8: each lane decodes 16 trellis positions of a tile
+//   gemv_kernel      rows 1..16: each lane decodes 16 trellis positions of a tile
 //                    straight into an fp16 MFMA A-fragment (W^T), the activations
 //                    H128(x*su) arrive pre-split into fp16 hi/lo halves in the 16
 //                    MFMA columns, v_mfma_f32_16x16x32_f16 accumulates in fp32;
@@ -547,7 +547,8 @@ struct GemvStream {
 };
 constexpr int kGemvPrepMax = 16;          // a workgroup preps at most kGemvPrepMax x waves (kb, row) blocks
 constexpr size_t kGemvDummyBytes = 8192;  // >= largest lane offset of a group + its K words (1024 K)
-constexpr size_t kGemvFragLds = 49152;    // LDS budget of the B fragments of a workgroup
+constexpr size_t kGemvFragLds = 49152;    // LDS budget of the B fragments of a workgroup (rows <= 8)
+constexpr size_t kGemvFragLds16 = 65536;  // the same for rows 9..16 (two workgroups still fit a CU)
 
 // K contiguous words of a chunk, in as few loads as its alignment allows
 template <int K>
@@ -574,7 +575,10 @@ __device__ __forceinline__ void load_chunk(const uint8_t *p, uint32_t (&w)[K]) {
     }
 }
 
-template <int K, int CB>
+// TWO (rows 9..16): a second block of B columns carries rows 8..15 (hi and lo as
+// for rows 0..7); each decoded A fragment feeds both blocks' MFMAs, so the decode
+// is shared by all 16 rows.
+template <int K, int CB, bool TWO>
 __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
     GemvTargets tg, int kbs, int nbs, int splits, const void *__restrict__ x, int x_f16, size_t x_stride, int rows,
     const uint8_t *__restrict__ dummy, float *__restrict__ partials, unsigned *__restrict__ counters, int y_f16) {
@@ -582,7 +586,9 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
     constexpr int P = W / 4;  // waves per column pair
     constexpr int NT = W * 64;
     constexpr size_t GB = (size_t)2048 * K + 512;
-    constexpr int D = GemvStream<K>::DEPTH;
+    // rows 9..16 need 8 more accumulator and fragment registers: a shorter ring at
+    // K <= 2 keeps them within 128 VGPRs (two workgroups per CU)
+    constexpr int D = TWO && K <= 2 ? 8 : GemvStream<K>::DEPTH;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ int last_flag;
     uint8_t *frag = smem;
@@ -774,8 +780,11 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
     // k group l / 16; rows >= `rows` read the last row (their columns are discarded)
     const int m = li, hl = m >> 3, mrow = (m & 7) < rows ? (m & 7) : rows - 1;
     const int boff = ((g * 2 + hl) * rows + mrow) * 16;
+    const int mrow2 = 8 + (m & 7) < rows ? 8 + (m & 7) : rows - 1;  // TWO: rows 8..15
+    const int boff2 = ((g * 2 + hl) * rows + mrow2) * 16;
     const bool first_chunk = j == 0;
     f4 acc1 = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
+    f4 acc3 = {0.f, 0.f, 0.f, 0.f}, acc4 = {0.f, 0.f, 0.f, 0.f};  // TWO: acc1 / acc2 of rows 8..15
     auto mac = [&](int i, const uint32_t (&w)[K]) {
         // last word of the previous chunk of the same tile: lane i - 1, or i + 7 for chunk 0
         const uint32_t p1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)w[K - 1], 0x121, 0xF, 0xF, false);  // row_ror:1
@@ -788,6 +797,14 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
         acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<h8>(fr[1]), bhi, acc1, 0, 0, 0);
         acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<h8>(fr[2]), blo, acc2, 0, 0, 0);
         acc2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<h8>(fr[3]), bhi, acc2, 0, 0, 0);
+        if constexpr (TWO) {
+            const uint8_t *bp2 = frag + (size_t)group_q(i) * 2 * blk_bytes + boff2;
+            const h8 clo = *(const h8 *)bp2, chi = *(const h8 *)(bp2 + blk_bytes);
+            acc3 = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<h8>(fr[0]), clo, acc3, 0, 0, 0);
+            acc3 = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<h8>(fr[1]), chi, acc3, 0, 0, 0);
+            acc4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<h8>(fr[2]), clo, acc4, 0, 0, 0);
+            acc4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<h8>(fr[3]), chi, acc4, 0, 0, 0);
+        }
     };
     int i0 = 0;
     for (; i0 + D <= ngroups; i0 += D) {  // full rounds: no branches between issue and use
@@ -819,9 +836,18 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
             rp[n < 8 ? n : 8 + n] = acc1[e] + o1;
             rp[n < 8 ? 8 + n : 16 + n] = acc2[e] + o2;
         }
+        if constexpr (TWO) {
+            const float o3 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc3[e]), 0x108, 0xF, 0xF, true));
+            const float o4 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc4[e]), 0x108, 0xF, 0xF, true));
+            if (m < 8 && 8 + m < rows) {
+                float *rp = red + part * nval + (8 + m) * 128 + 32 * cp;
+                rp[n < 8 ? n : 8 + n] = acc3[e] + o3;
+                rp[n < 8 ? 8 + n : 16 + n] = acc4[e] + o4;
+            }
+        }
     }
     __syncthreads();
-    constexpr int PER = (kGemvMaxRows * 128 + NT - 1) / NT;
+    constexpr int PER = ((TWO ? 16 : 8) * 128 + NT - 1) / NT;
     float psum[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
@@ -930,7 +956,7 @@ GemvPlan gemv_plan(size_t k, size_t n, size_t rows) {
     // most kGemvPrepMax (kb, row) blocks; one kb per workgroup always fits
     for (;;) {
         const size_t nkb = ((size_t)p.kbs + s - 1) / s;
-        const bool ok_lds = nkb * 512 * rows <= kGemvFragLds;
+        const bool ok_lds = nkb * 512 * rows <= (rows > 8 ? kGemvFragLds16 : kGemvFragLds);
         const bool ok_prep = (nkb * rows + kGemvWaves - 1) / kGemvWaves <= (size_t)kGemvPrepMax;
         if ((ok_lds && ok_prep) || s >= p.kbs) break;
         ++s;
@@ -953,9 +979,16 @@ static hipError_t launch_gemv_kc(const GemvTargets &tg, const void *x, int x_f16
                                  int y_f16, uint8_t *ws, const GemvPlan &p, hipStream_t stream) {
     const size_t lds = gemv_lds_bytes(p.nkw, rows);
     const dim3 grid((unsigned)(p.nbs * p.splits)), block(kGemvWaves * 64);
-    gemv_kernel<K, CB><<<grid, block, lds, stream>>>(tg, p.kbs, p.nbs, p.splits, x, x_f16, x_stride, (int)rows,
-                                                     ws + p.dummy_off, (float *)(ws + p.partials_off),
-                                                     (unsigned *)(ws + p.counters_off), y_f16);
+    if (rows > 8)
+        gemv_kernel<K, CB, true><<<grid, block, lds, stream>>>(tg, p.kbs, p.nbs, p.splits, x, x_f16, x_stride,
+                                                               (int)rows, ws + p.dummy_off,
+                                                               (float *)(ws + p.partials_off),
+                                                               (unsigned *)(ws + p.counters_off), y_f16);
+    else
+        gemv_kernel<K, CB, false><<<grid, block, lds, stream>>>(tg, p.kbs, p.nbs, p.splits, x, x_f16, x_stride,
+                                                                (int)rows, ws + p.dummy_off,
+                                                                (float *)(ws + p.partials_off),
+                                                                (unsigned *)(ws + p.counters_off), y_f16);
     return hipGetLastError();
 }
 

@@ -9,7 +9,7 @@
 
 namespace exl3k {
 
-constexpr int kGemvMaxRows = 8;   // GEMV packs hi/lo fp16 halves of up to 8 rows into 16 MFMA columns
+constexpr int kGemvMaxRows = 16;  // GEMV: hi/lo fp16 halves of 8 rows per 16 MFMA columns, two column blocks
 constexpr int kGemvWaves = 8;     // waves per GEMV workgroup (a multiple of 4)
 constexpr int kGemmWaves = 4;
 
