@@ -250,3 +250,31 @@ def test_group_matches_single_layers(amd, oracle, rows):
                 assert np.array_equal(y, single)
     L = amd.lib()
     assert L.exl3_hip_mul_mat_group(None, 1, 4, 2, 2048, None, 1, 1, 2048, 1, None, 0, None) == 1
+
+
+def test_concurrent_streams(amd):
+    """Calls interleaved on two streams (default priority) at once: with internal
+    workspaces (one per device and stream) and with a caller workspace per stream,
+    every result equals the same call made alone (the layer is deterministic)."""
+    import torch
+    k, n, bits = 4096, 2048, 4
+    recs = [dev(make_layer(900 + i, k, n, bits)) for i in range(2)]
+    row_counts = (1, 8, 13, 40)
+    xs = [torch.from_numpy(synth.activations(910 + r, r, k)).cuda() for r in row_counts]
+    ref = [[amd.mul_mat(recs[i], bits, k, n, x).clone() for x in xs] for i in range(2)]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    wss = [amd.new_workspace(k, n, max(row_counts)) for _ in range(2)]
+    torch.cuda.synchronize()
+    for use_ws in (False, True):
+        for rep in range(3):
+            outs = [[None] * len(xs) for _ in range(2)]
+            for j, x in enumerate(xs):
+                for i in range(2):
+                    with torch.cuda.stream(streams[i]):
+                        outs[i][j] = amd.mul_mat(recs[i], bits, k, n, x, stream=streams[i],
+                                                 workspace=wss[i] if use_ws else None)
+            torch.cuda.synchronize()
+            for i in range(2):
+                for j, r in enumerate(row_counts):
+                    assert torch.equal(outs[i][j], ref[i][j]), f"stream {i} rows={r} rep={rep} ws={use_ws}"
