@@ -223,7 +223,7 @@ def main():
                    "k": K_IN, "n": N_OUT, "bits": BITS, "rows": 1, "weight_copies": COPIES},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "kernel": "exl3k::gemv_kernel<4,2>", "kernel_us_mean": round(ms1 * 1e3, 3),
+                     "kernel": "exl3k::gemv_kernel<4,2,false>", "kernel_us_mean": round(ms1 * 1e3, 3),
                      "algorithmic_bytes": b1},
         "cpu_baseline": cpu,
     }
