@@ -168,8 +168,9 @@ __device__ __forceinline__ void decode_block(const uint8_t *__restrict__ src, in
         const int row = ch >> 5, col8 = ch & 31;
         const int tl2 = col8 >> 1;
         if (t0 + tl2 < tile_count) {
-            const uint4 v = *(const uint4 *)(tb + row * PITCH + col8 * 8);
-            *(uint4 *)(out + (rk * 16 + row) * count + (t0 + tl2) * 16 + (col8 & 1) * 8) = v;
+            const u4 v = *(const u4 *)(tb + row * PITCH + col8 * 8);
+            // streaming store: the fp16 output is written once and not read back here
+            __builtin_nontemporal_store(v, (u4 *)(out + (rk * 16 + row) * count + (t0 + tl2) * 16 + (col8 & 1) * 8));
         }
     }
 }
