@@ -106,7 +106,7 @@ def test_f32_input_and_strides(amd, oracle):
     k, n, bits = 512, 256, 3
     rec = make_layer(600, k, n, bits)
     rd = dev(rec)
-    for rows in (5, 20):
+    for rows in (5, 11, 20):
         x16 = synth.activations(601, rows, k)
         ref = oracle.mul_mat(rec, bits, 2, k, n, x16)
         xpad = np.zeros((rows, k + 64), np.float32)
@@ -172,7 +172,7 @@ def test_linearity_full_size(amd):
         assert_layer_close(ys[2], ys[0] + ys[1], what=f"linearity rows={rows}")
 
 
-@pytest.mark.parametrize("rows", [1, 5, 37])
+@pytest.mark.parametrize("rows", [1, 5, 14, 37])
 def test_graph_replay_matches_eager(amd, oracle, rows):
     """A HIP graph of mul_mat calls (split-K counters self-reset, no memset
     nodes) replays bit-identically, with eager work between the replays."""
