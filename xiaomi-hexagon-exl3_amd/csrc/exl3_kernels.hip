@@ -581,8 +581,9 @@ __device__ __forceinline__ void load_chunk(const uint8_t *p, uint32_t (&w)[K]) {
 // is shared by all 16 rows.
 template <int K, int CB, bool TWO>
 __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
-    GemvTargets tg, int kbs, int nbs, int splits, const void *__restrict__ x, int x_f16, size_t x_stride, int rows,
-    const uint8_t *__restrict__ dummy, float *__restrict__ partials, unsigned *__restrict__ counters, int y_f16) {
+    GemvTargets tg, int kbs, int splits, int kq, int kr, const void *__restrict__ x, int x_f16, size_t x_stride,
+    int rows, const uint8_t *__restrict__ dummy, float *__restrict__ partials, unsigned *__restrict__ counters,
+    int y_f16) {
     constexpr int W = kGemvWaves;
     constexpr int P = W / 4;  // waves per column pair
     constexpr int NT = W * 64;
@@ -598,8 +599,10 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int cp = wave & 3, part = wave >> 2;
-    const int s = blockIdx.x / nbs, nb = blockIdx.x - s * nbs;
-    const int kb0 = (int)((long long)kbs * s / splits), kb1 = (int)((long long)kbs * (s + 1) / splits);
+    // grid (column group, split): no division on the way to the first loads.
+    // Split s owns kq + (s < kr) records from kb0 (kq = kbs / splits, kr = kbs % splits)
+    const int nb = blockIdx.x, s = blockIdx.y;
+    const int kb0 = s * kq + (s < kr ? s : kr), kb1 = kb0 + kq + (s < kr ? 1 : 0);
     const int nkb = kb1 - kb0;
     // the matrix of column group nb (targets share k, x and the bit rate)
     int mi = 0;
@@ -979,14 +982,16 @@ template <int K, int CB>
 static hipError_t launch_gemv_kc(const GemvTargets &tg, const void *x, int x_f16, size_t rows, size_t x_stride,
                                  int y_f16, uint8_t *ws, const GemvPlan &p, hipStream_t stream) {
     const size_t lds = gemv_lds_bytes(p.nkw, rows);
-    const dim3 grid((unsigned)(p.nbs * p.splits)), block(kGemvWaves * 64);
+    // x fastest: workgroup (nb, s) is dispatched as nb + s nbs, as a 1-D grid would be
+    const dim3 grid((unsigned)p.nbs, (unsigned)p.splits), block(kGemvWaves * 64);
+    const int kq = p.kbs / p.splits, kr = p.kbs % p.splits;
     if (rows > 8)
-        gemv_kernel<K, CB, true><<<grid, block, lds, stream>>>(tg, p.kbs, p.nbs, p.splits, x, x_f16, x_stride,
+        gemv_kernel<K, CB, true><<<grid, block, lds, stream>>>(tg, p.kbs, p.splits, kq, kr, x, x_f16, x_stride,
                                                                (int)rows, ws + p.dummy_off,
                                                                (float *)(ws + p.partials_off),
                                                                (unsigned *)(ws + p.counters_off), y_f16);
     else
-        gemv_kernel<K, CB, false><<<grid, block, lds, stream>>>(tg, p.kbs, p.nbs, p.splits, x, x_f16, x_stride,
+        gemv_kernel<K, CB, false><<<grid, block, lds, stream>>>(tg, p.kbs, p.splits, kq, kr, x, x_f16, x_stride,
                                                                 (int)rows, ws + p.dummy_off,
                                                                 (float *)(ws + p.partials_off),
                                                                 (unsigned *)(ws + p.counters_off), y_f16);
@@ -1247,9 +1252,9 @@ __device__ __forceinline__ void gemm_rows_out(float (&t)[4][NE], int lane, int r
 
 template <int K, int CB, int RB>
 __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
-    const uint8_t *__restrict__ records, int kbs, int nbs, int mtiles, int splits, const uint16_t *__restrict__ xh16,
-    size_t k, uint16_t *__restrict__ partials, void *y, int y_f16, size_t y_stride, int rows, const void *res,
-    size_t res_stride) {
+    const uint8_t *__restrict__ records, int kbs, int nbs, int mtiles, int splits, int kq, int kr,
+    const uint16_t *__restrict__ xh16, size_t k, uint16_t *__restrict__ partials, void *y, int y_f16, size_t y_stride,
+    int rows, const void *res, size_t res_stride) {
     constexpr int BM = 32 * RB * kGemmWaves;
     constexpr size_t GB = (size_t)2048 * K + 512;
     __shared__ __attribute__((aligned(16))) uint16_t wlds[2][128 * 128];  // 64 KB
@@ -1269,7 +1274,8 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
     L -= s * mtiles * nbs;
     const int nb = L / mtiles, mt = L - nb * mtiles;
     const int tile = mt * nbs + nb;
-    const int kb0 = (int)((long long)kbs * s / splits), kb1 = (int)((long long)kbs * (s + 1) / splits);
+    // split s owns kq + (s < kr) records from kb0 (kq = kbs / splits, kr = kbs % splits, from the host)
+    const int kb0 = s * kq + (s < kr ? s : kr), kb1 = kb0 + kq + (s < kr ? 1 : 0);
     const uint8_t *colgroup = records + (size_t)nb * kbs * GB;
 
     // weights: this wave decodes groups q = 2 wave + h (h = 0, 1) of every record
@@ -1532,16 +1538,17 @@ static void launch_gemm_kc(const uint8_t *rec, size_t k, uint16_t *xh, size_t ro
     const dim3 grid((unsigned)(p.mtiles * p.nbs * p.splits)), block(kGemmWaves * 64);
     uint16_t *part = (uint16_t *)(ws + p.partials_off);
     const int nwaves = p.mtiles * p.nbs * (p.bm / 16);  // reduction: one wave per 16 rows of a tile
+    const int kq = p.kbs / p.splits, kr = p.kbs % p.splits;
     const dim3 rgrid((unsigned)((nwaves + 3) / 4));
     if (p.bm == 128) {
-        gemm_kernel<K, CB, 1><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, xh, k, part, y, y_f16,
-                                                          y_stride, (int)rows, res, res_stride);
+        gemm_kernel<K, CB, 1><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, kq, kr, xh, k, part,
+                                                          y, y_f16, y_stride, (int)rows, res, res_stride);
         if (p.splits > 1)
             gemm_reduce_kernel<1><<<rgrid, dim3(256), 0, stream>>>(part, p.splits, p.nbs, rec, K, p.kbs, y, y_f16,
                                                                    y_stride, (int)rows, nwaves, res, res_stride);
     } else {
-        gemm_kernel<K, CB, 2><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, xh, k, part, y, y_f16,
-                                                          y_stride, (int)rows, res, res_stride);
+        gemm_kernel<K, CB, 2><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, kq, kr, xh, k, part,
+                                                          y, y_f16, y_stride, (int)rows, res, res_stride);
         if (p.splits > 1)
             gemm_reduce_kernel<2><<<rgrid, dim3(256), 0, stream>>>(part, p.splits, p.nbs, rec, K, p.kbs, y, y_f16,
                                                                    y_stride, (int)rows, nwaves, res, res_stride);
