@@ -207,6 +207,24 @@ __device__ __forceinline__ float dpp_xor(float v) {
     }
 }
 
+// Layout of an H128 block spread over a 16-lane row with 8 consecutive elements
+// per lane: lane l holds elements 8 b .. 8 b + 7 with b = h128_lane_block(l) =
+// (l0 ^ l2, l1 ^ l2, l2, l3) in bits (an involution).  The cross-lane stages over
+// block bits 1, 2, 4, 8 then pair lane l with l ^ 1, l ^ 2, l ^ 7 and l ^ 8, each
+// one DPP read (xor 7 is row_half_mirror) where plain order needs two bank-masked
+// reads and a copy for xor 4.
+__device__ __forceinline__ int h128_lane_block(int l) { return l ^ (((l >> 2) & 1) * 3); }
+
+// Value of the lane holding block b ^ S (S = 1, 2, 4, 8) in that layout.
+template <int S>
+__device__ __forceinline__ float dpp_block_xor(float v) {
+    if constexpr (S == 4) {
+        return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));  // row_half_mirror
+    } else {
+        return dpp_xor<S>(v);
+    }
+}
+
 // H128 of one 128-block held by a wave: lane l owns element l in v0 and element
 // l + 64 in v1.  Stages 1..32 pair lanes l and l ^ step, stage 64 pairs v0/v1;
 // each butterfly is (a + b, a - b) with a the lower index, in the reference's

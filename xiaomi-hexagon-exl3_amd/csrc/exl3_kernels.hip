@@ -646,11 +646,11 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
 
     // 1-2. prep: xh = H128(x[r] su) per (kb, row) block of the workgroup, as
     // fp16 hi = rn(xh) and lo = rn(xh - hi) into the B fragments.  Unit q of
-    // wave w is up to four blocks (block = kbl rows + r): lane 16 g + i holds
-    // elements 8 i .. 8 i + 7 of block (4 q + g) W + w (blocks dealt across the
-    // waves first, so a few blocks still run on as many waves): H128 stages 1,
-    // 2, 4 inside the lane, 8 .. 64 across lanes i ^ 1 .. 8 by DPP, in the
-    // reference's stage order.
+    // wave w is up to four blocks (block = kbl rows + r): lane 16 g + l holds
+    // elements 8 i .. 8 i + 7, i = h128_lane_block(l), of block (4 q + g) W + w
+    // (blocks dealt across the waves first, so a few blocks still run on as many
+    // waves): H128 stages 1, 2, 4 inside the lane, 8 .. 64 with the lanes holding
+    // i ^ 1, 2, 4, 8 (one DPP read each), in the reference's stage order.
     // Elements 8 i .. 8 i + 7 are one 16-byte slot of the fragment blocks (tile
     // row 4 (i / 8) + (i / 2) % 4 ... : r4 = i / 8, kg = (i / 2) % 4, half = i % 2),
     // so a lane stores hi and lo with one 16-byte write each.  NQ (units per
@@ -661,7 +661,7 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
     auto prologue = [&](auto nq_c, auto is_f16) {
         constexpr int NQ = decltype(nq_c)::value;
         constexpr bool XF16 = decltype(is_f16)::value;
-        const int pi = lane & 15;
+        const int pi = h128_lane_block(lane & 15);  // this lane's 8-element block of each unit
         uint4 xr[NQ][XF16 ? 1 : 2], sr[NQ];
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
@@ -708,7 +708,7 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
                     const float sgn = (pi & S) ? -1.f : 1.f;
                     float pv[8];
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) pv[j] = dpp_xor<S>(v[j]);
+                    for (int j = 0; j < 8; ++j) pv[j] = dpp_block_xor<S>(v[j]);
 #pragma unroll
                     for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(v[j], sgn, pv[j]);
                 };
@@ -1050,10 +1050,11 @@ __host__ __device__ inline size_t gemm_xh_offset(int row, int kb, int e, int kbs
     const int ln = (row & 31) + 32 * (kk >> 3);
     return ((((size_t)(row >> 5) * kbs + kb) * 8 + ks) * 64 + ln) * 8 + (kk & 7);
 }
-// Workgroup (kb, rb), 4 waves x 8 rows (two passes of 4); lane 16 g + i holds
-// elements 8 i .. 8 i + 7 of row 32 rb + 8 wave + 4 pass + g.  H128 stages 1, 2
-// and 4 are inside the lane, 8 .. 64 pair lanes i ^ 1 .. 8 (DPP); the lane's
-// eight results are one 16-byte unit of the fragment layout, stored directly.
+// Workgroup (kb, rb), 4 waves x 8 rows (two passes of 4); lane 16 g + l holds
+// elements 8 i .. 8 i + 7, i = h128_lane_block(l), of row 32 rb + 8 wave + 4 pass
+// + g.  H128 stages 1, 2 and 4 are inside the lane, 8 .. 64 pair it with the
+// lanes holding i ^ 1 .. 8 (one DPP read each); the lane's eight results are one
+// 16-byte unit of the fragment layout, stored directly.
 template <bool XF16>
 __device__ __forceinline__ void xprep_load(const void *__restrict__ x, const size_t (&off)[2], float (&v)[2][8]) {
 #pragma unroll
@@ -1072,7 +1073,8 @@ __device__ __forceinline__ void xprep_load(const void *__restrict__ x, const siz
 __global__ __launch_bounds__(256) void gemm_xprep_kernel(const uint8_t *__restrict__ records, int bits,
                                                          const void *__restrict__ x, int x_f16, size_t x_stride,
                                                          int rows, int kbs, uint16_t *__restrict__ xh16) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, i = lane & 15;
+    // i: this lane's 8-element block of the row (h128_lane_block order)
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, i = h128_lane_block(lane & 15);
     const int kb = blockIdx.x, rb = blockIdx.y;
     const size_t col = (size_t)kb * 128 + 8 * i;
     const uint4 su8 = *(const uint4 *)(records + (size_t)kb * group_bytes(bits) + 2048 * bits + 16 * i);
@@ -1113,7 +1115,7 @@ __global__ __launch_bounds__(256) void gemm_xprep_kernel(const uint8_t *__restri
 #pragma unroll
         for (int ps = 0; ps < 2; ++ps)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) p[ps][j] = dpp_xor<S>(v[ps][j]);
+            for (int j = 0; j < 8; ++j) p[ps][j] = dpp_block_xor<S>(v[ps][j]);
 #pragma unroll
         for (int ps = 0; ps < 2; ++ps)
 #pragma unroll
