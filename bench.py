@@ -409,6 +409,34 @@ def cpu_baseline(np, synth):
 
     t_all = med(cores, 5)
     t_one = med(1, 3)
+
+    # decode only (the CPU side of the dequant sweep): the oracle's decode_inner on
+    # one MLP matrix, on one thread as the reference runs it, and in column slices
+    # on all cores (ctypes releases the GIL during each call)
+    from concurrent.futures import ThreadPoolExecutor
+    kd, nd, bd = 2048, 6144, 4
+    pd = synth.packed_tiles(78, kd, nd, bd)
+    dbytes = kd * nd * bd // 8 + 2 * kd * nd
+    width = max(16, nd // cores // 16 * 16)
+    slices = [(f, min(width, nd - f)) for f in range(0, nd, width)]
+
+    def dec_med(threads, reps):
+        def once():
+            if threads == 1:
+                orc.decode_inner(pd, kd, nd, bd, CB)
+            else:
+                with ThreadPoolExecutor(threads) as ex:
+                    list(ex.map(lambda sl: orc.decode_inner(pd, kd, nd, bd, CB, first=sl[0], count=sl[1]), slices))
+        once()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            once()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
+    td_all = dec_med(cores, 5)
+    td_one = dec_med(1, 3)
     cpu_model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -421,7 +449,12 @@ def cpu_baseline(np, synth):
             "sample": f"full k=14336 x n=4096 4-bpw layer, batch 1, oracle restatement of ggml_exl3_mul_mat, "
                       f"{cores} threads (ggml nb partition), median of 5 after 1 warm-up; cpu {cpu_model}",
             "ms": round(t_all * 1e3, 2), "single_thread_gbps": round(b1 / t_one / 1e9, 3),
-            "single_thread_ms": round(t_one * 1e3, 1)}
+            "single_thread_ms": round(t_one * 1e3, 1),
+            "decode": {"sample": f"decode_inner restatement, k=2048 x n=6144 at 4 bits (one MLP matrix of the "
+                                 f"dequant sweep), {len(slices)} column slices on {cores} threads; median of 5 / 3",
+                       "gbps": round(dbytes / td_all / 1e9, 3), "ms": round(td_all * 1e3, 2),
+                       "single_thread_gbps": round(dbytes / td_one / 1e9, 3),
+                       "single_thread_ms": round(td_one * 1e3, 1)}}
 
 
 if __name__ == "__main__":
