@@ -31,7 +31,7 @@ def test_library_loads_and_exports_c_abi():
     assert not missing, missing
     assert set(amd.EXPORTS) == set(declared)
     assert amd.lib().exl3_hip_version() == 10000
-    assert amd.lib().exl3_hip_gemv_max_rows() == 16
+    assert amd.lib().exl3_hip_gemv_max_rows() == 32
 
 
 def test_library_exports_codec_api():

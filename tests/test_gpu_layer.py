@@ -56,26 +56,28 @@ def test_all_rates_and_codebooks(amd, oracle, bits):
     rec = make_layer(bits * 31, k, n, bits)
     rd = dev(rec)
     for cb in range(3):
-        for rows in (1, 3, 8, 12):
+        for rows in (1, 3, 8, 12, 24):
             x = synth.activations(bits * 100 + cb * 10 + rows, rows, k)
             ref = oracle.mul_mat(rec, bits, cb, k, n, x)
             assert_layer_close(run(amd, rd, bits, k, n, x, cb), ref, what=f"bits={bits} cb={cb} rows={rows}")
 
 
-@pytest.mark.parametrize("rows", [1, 2, 4, 8, 9, 12, 16])
+@pytest.mark.parametrize("rows", [1, 2, 4, 8, 9, 12, 16, 17, 24, 32])
 def test_c3_full_size_gemv(amd, oracle, rows):
     """4096 x 14336 at 4 bits (k=14336 in, n=4096 out), ragged decode batches up to the
-    GEMV's 16 rows (rows 9..16 use its second block of MFMA columns)"""
+    GEMV's 32 rows (rows 9..16 use its second block of MFMA columns, rows 17..32 fp16
+    activations prepared once per call)"""
     k, n, bits = 14336, 4096, 4
     rec = make_layer(303, k, n, bits)
     x = synth.activations(304 + rows, rows, k)
     ref = oracle.mul_mat(rec, bits, 2, k, n, x, threads=THREADS)
     y = run(amd, dev(rec), bits, k, n, x)
     ma, rl = assert_layer_close(y, ref, what=f"C3 rows={rows}")
-    assert rl < 1e-5  # hi/lo activation split keeps the GEMV at fp32-level accuracy
+    if rows <= 16:
+        assert rl < 1e-5  # hi/lo activation split keeps the GEMV at fp32-level accuracy
 
 
-@pytest.mark.parametrize("rows", [17, 32, 37, 128, 300])
+@pytest.mark.parametrize("rows", [33, 37, 128, 300])
 def test_gemm_rows(amd, oracle, rows):
     k, n, bits = 1024, 384, 4
     rec = make_layer(400 + rows, k, n, bits)
@@ -106,7 +108,7 @@ def test_f32_input_and_strides(amd, oracle):
     k, n, bits = 512, 256, 3
     rec = make_layer(600, k, n, bits)
     rd = dev(rec)
-    for rows in (5, 11, 20):
+    for rows in (5, 11, 20, 40):
         x16 = synth.activations(601, rows, k)
         ref = oracle.mul_mat(rec, bits, 2, k, n, x16)
         xpad = np.zeros((rows, k + 64), np.float32)
@@ -215,7 +217,7 @@ def test_one_workspace_serves_mixed_row_counts(amd):
     import torch
     k, n, bits = 2048, 4096, 4
     rd = dev(make_layer(820, k, n, bits))
-    seq = [300, 100, 300, 5, 300, 1, 37, 300, 8, 129, 16, 11, 300, 9]
+    seq = [300, 100, 300, 5, 300, 1, 37, 300, 8, 129, 16, 11, 300, 9, 32, 20, 300, 17]
     xs = {r: torch.from_numpy(synth.activations(821 + r, r, k)).cuda() for r in set(seq)}
     fresh = {}
     for r in set(seq):
@@ -231,11 +233,12 @@ def test_one_workspace_serves_mixed_row_counts(amd):
         assert torch.equal(y_internal, fresh[r]), f"internal workspace, call {i} rows={r}"
 
 
-@pytest.mark.parametrize("rows", [1, 3, 8, 12, 16, 20])
+@pytest.mark.parametrize("rows", [1, 3, 8, 12, 16, 20, 32, 40])
 def test_group_matches_single_layers(amd, oracle, rows):
-    """q/k/v and gate/up of one decoder layer through exl3_hip_mul_mat_group: one launch
-    (rows <= 16, the GEMV) that serves several matrices sharing x; each output within the
-    layer tolerance of the oracle, and above (one call per matrix) equal to mul_mat"""
+    """q/k/v and gate/up of one decoder layer through exl3_hip_mul_mat_group: one GEMV
+    launch (rows <= 32; above 16 after one activation pass for all matrices) that serves
+    several matrices sharing x; each output within the layer tolerance of the oracle,
+    and above (one call per matrix) equal to mul_mat"""
     import torch
     for k, shapes, bits in [(2048, [2048, 512, 512], 6), (2048, [6144, 6144], 4)]:
         recs = [make_layer(700 + i + bits, k, n, bits) for i, n in enumerate(shapes)]

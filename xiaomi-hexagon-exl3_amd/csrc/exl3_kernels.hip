@@ -576,14 +576,19 @@ __device__ __forceinline__ void load_chunk(const uint8_t *p, uint32_t (&w)[K]) {
     }
 }
 
-// TWO (rows 9..16): a second block of B columns carries rows 8..15 (hi and lo as
+// MODE 0 (rows 1..8): one block of 16 B columns, hi and lo of 8 rows.
+// MODE 1 (rows 9..16): a second block of B columns carries rows 8..15 (hi and lo as
 // for rows 0..7); each decoded A fragment feeds both blocks' MFMAs, so the decode
 // is shared by all 16 rows.
-template <int K, int CB, bool TWO>
+// MODE 2 (rows 17..32): two blocks of 16 rows each, fp16 activations without the
+// lo halves, prepared once per call by gemv_xprep_kernel (xpre) and copied into
+// LDS instead of being transformed again by every column group.
+template <int K, int CB, int MODE>
 __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
     GemvTargets tg, int kbs, int splits, int kq, int kr, const void *__restrict__ x, int x_f16, size_t x_stride,
     int rows, const uint8_t *__restrict__ dummy, float *__restrict__ partials, unsigned *__restrict__ counters,
-    int y_f16) {
+    int y_f16, const uint8_t *__restrict__ xpre) {
+    constexpr bool TWO = MODE >= 1, HILO = MODE <= 1;
     constexpr int W = kGemvWaves;
     constexpr int P = W / 4;  // waves per column pair
     constexpr int NT = W * 64;
@@ -594,7 +599,8 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ int last_flag;
     uint8_t *frag = smem;
-    const int blk_bytes = 128 * rows;  // B fragments of one (kb, r4, half): [kg][hl][row] x 16 bytes
+    // B fragments of one (kb, r4, half): [kg][hl][row] x 16 bytes (MODE 2: [kg][row])
+    const int blk_bytes = (HILO ? 128 : 64) * rows;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -773,8 +779,27 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
         else if (nq <= 2) prologue(std::integral_constant<int, 2>{}, is_f16);
         else prologue(std::integral_constant<int, 4>{}, is_f16);
     };
-    if (x_f16) prologue_x(std::true_type{});
-    else prologue_x(std::false_type{});
+    if constexpr (MODE == 2) {
+        // the workgroup's records [kb0, kb1) of the target's prepared activations,
+        // laid out exactly as the LDS fragments: one contiguous copy, all loads first
+        const uint8_t *src = xpre + ((size_t)mi * kbs + kb0) * (size_t)(4 * blk_bytes);
+        const int nbytes = nkb * 4 * blk_bytes;  // <= kGemvFragLds16
+        constexpr int CPY = (int)(kGemvFragLds16 / (NT * 16));
+        u4 cv[CPY];
+#pragma unroll
+        for (int c = 0; c < CPY; ++c) {
+            const int o = (c * NT + tid) * 16;
+            if (o < nbytes) cv[c] = *(const u4 *)(src + o);
+        }
+#pragma unroll
+        for (int c = 0; c < CPY; ++c) {
+            const int o = (c * NT + tid) * 16;
+            if (o < nbytes) *(u4 *)(frag + o) = cv[c];
+        }
+    } else {
+        if (x_f16) prologue_x(std::true_type{});
+        else prologue_x(std::false_type{});
+    }
     const float sv0 = half_bits_to_float(svp[lane]), sv1 = half_bits_to_float(svp[lane + 64]);
     __syncthreads();
 #pragma unroll
@@ -782,10 +807,12 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
 
     // 4. decode + MFMA.  B operand lane l: m = l % 16 -> (hl, row) = (m / 8, m % 8),
     // k group l / 16; rows >= `rows` read the last row (their columns are discarded)
-    const int m = li, hl = m >> 3, mrow = (m & 7) < rows ? (m & 7) : rows - 1;
-    const int boff = ((g * 2 + hl) * rows + mrow) * 16;
-    const int mrow2 = 8 + (m & 7) < rows ? 8 + (m & 7) : rows - 1;  // TWO: rows 8..15
-    const int boff2 = ((g * 2 + hl) * rows + mrow2) * 16;
+    // (MODE 2: m -> row m, and row 16 + m in the second block)
+    const int m = li, hl = m >> 3;
+    const int r1 = HILO ? (m & 7) : m, r2 = HILO ? 8 + (m & 7) : 16 + m;
+    const int mrow = r1 < rows ? r1 : rows - 1, mrow2 = r2 < rows ? r2 : rows - 1;  // TWO: the second block
+    const int boff = (HILO ? (g * 2 + hl) * rows + mrow : g * rows + mrow) * 16;
+    const int boff2 = (HILO ? (g * 2 + hl) * rows + mrow2 : g * rows + mrow2) * 16;
     const bool first_chunk = j == 0;
     f4 acc1 = {0.f, 0.f, 0.f, 0.f}, acc2 = {0.f, 0.f, 0.f, 0.f};
     f4 acc3 = {0.f, 0.f, 0.f, 0.f}, acc4 = {0.f, 0.f, 0.f, 0.f};  // TWO: acc1 / acc2 of rows 8..15
@@ -826,12 +853,26 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
         if (i0 + d < ngroups) mac(i0 + d, buf[d]);
 
     // 5. epilogue: hi + lo (MFMA column m < 8 gets column m + 8) into this wave's
-    // 32 columns of its share of the workgroup partial
+    // 32 columns of its share of the workgroup partial (MODE 2: column m is row m)
     __syncthreads();  // every wave is done with the fragments; LDS now holds the partials
     float *red = (float *)smem;  // [P][rows][128]
     const int nval = rows * 128;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 0; e < 4 && !HILO; ++e) {
+        const int n = 4 * g + e;
+        if (m < rows) {
+            float *rp = red + part * nval + m * 128 + 32 * cp;
+            rp[n < 8 ? n : 8 + n] = acc1[e];
+            rp[n < 8 ? 8 + n : 16 + n] = acc2[e];
+        }
+        if (16 + m < rows) {
+            float *rp = red + part * nval + (16 + m) * 128 + 32 * cp;
+            rp[n < 8 ? n : 8 + n] = acc3[e];
+            rp[n < 8 ? 8 + n : 16 + n] = acc4[e];
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 4 && HILO; ++e) {
         const int n = 4 * g + e;
         const float o1 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc1[e]), 0x108, 0xF, 0xF, true));
         const float o2 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc2[e]), 0x108, 0xF, 0xF, true));
@@ -851,7 +892,7 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
         }
     }
     __syncthreads();
-    constexpr int PER = ((TWO ? 16 : 8) * 128 + NT - 1) / NT;
+    constexpr int PER = ((MODE == 2 ? 32 : MODE == 1 ? 16 : 8) * 128 + NT - 1) / NT;
     float psum[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
@@ -937,10 +978,49 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
     for (int rr = wave; rr < rows; rr += W) finish_row(rr, ybuf[rr * 128 + lane], ybuf[rr * 128 + lane + 64]);
 }
 
+// Activations of the 17..32-row GEMV (MODE 2): fp16(H128(x[r] su)), su from record
+// (0, kb) of target t (src/exl3-ggml.cpp:60-73), in gemv_kernel's LDS fragment
+// order without lo halves: [t][kb][r4][half][kg][row] x 16 bytes.  One wave per
+// (row, kb, target); lane l holds elements 2 l and 2 l + 1 (h128_pair).
+__global__ __launch_bounds__(256) void gemv_xprep_kernel(GemvTargets tg, int bits, const void *__restrict__ x,
+                                                         int x_f16, size_t x_stride, int rows, int kbs,
+                                                         uint16_t *__restrict__ xpre) {
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), kb = blockIdx.y, t = blockIdx.z;
+    if (r >= rows) return;  // whole waves
+    const uint8_t *records = tg.records[0];
+#pragma unroll
+    for (int i = 1; i < kGemvMaxTargets; ++i)
+        if (t == i) records = tg.records[i];
+    const uint32_t ps = ((const uint32_t *)(records + (size_t)kb * group_bytes(bits) + 2048 * bits))[lane];
+    const size_t xi = (size_t)r * x_stride + (size_t)kb * 128 + 2 * lane;
+    float a, b;
+    if (x_f16) {
+        a = half_bits_to_float(((const uint16_t *)x)[xi]);
+        b = half_bits_to_float(((const uint16_t *)x)[xi + 1]);
+    } else {
+        a = ((const float *)x)[xi];
+        b = ((const float *)x)[xi + 1];
+    }
+    a *= half_bits_to_float((uint16_t)(ps & 0xffffu));
+    b *= half_bits_to_float((uint16_t)(ps >> 16));
+    h128_pair(a, b, lane);
+    // elements 2 lane (+1): r4 = lane / 32, kg = lane / 8 % 4, half = lane / 4 % 2,
+    // position 2 (lane % 4) (+1) of the 16-byte slot
+    const int r4 = lane >> 5, kg = (lane >> 3) & 3, half = (lane >> 2) & 1;
+    uint16_t *dst = xpre + ((((size_t)t * kbs + kb) * 2 + r4) * 2 + half) * (size_t)(32 * rows) + (kg * rows + r) * 8 +
+                    2 * (lane & 3);
+    *(uint32_t *)dst = (uint32_t)float_to_half_bits(a) | ((uint32_t)float_to_half_bits(b) << 16);
+}
+
+// B-fragment bytes of one record in a GEMV workgroup's LDS (hi and lo halves up to
+// 16 rows, fp16 only above)
+static size_t gemv_frag_bytes_per_kb(size_t rows) { return (rows > 16 ? 256 : 512) * rows; }
+
 // LDS bytes of a GEMV workgroup: its B fragments, reused after the main loop for
 // the P partials and the output rows
 static size_t gemv_lds_bytes(int nkb_max, size_t rows) {
-    const size_t frag = (size_t)nkb_max * 512 * rows;
+    const size_t frag = (size_t)nkb_max * gemv_frag_bytes_per_kb(rows);
     const size_t red = (size_t)(kGemvWaves / 4 + 1) * rows * 128 * 4;
     return ((frag > red ? frag : red) + 15) & ~(size_t)15;
 }
@@ -960,8 +1040,9 @@ GemvPlan gemv_plan(size_t k, size_t n, size_t rows) {
     // most kGemvPrepMax (kb, row) blocks; one kb per workgroup always fits
     for (;;) {
         const size_t nkb = ((size_t)p.kbs + s - 1) / s;
-        const bool ok_lds = nkb * 512 * rows <= (rows > 8 ? kGemvFragLds16 : kGemvFragLds);
-        const bool ok_prep = (nkb * rows + kGemvWaves - 1) / kGemvWaves <= (size_t)kGemvPrepMax;
+        const bool ok_lds = nkb * gemv_frag_bytes_per_kb(rows) <= (rows > 8 ? kGemvFragLds16 : kGemvFragLds);
+        // above 16 rows the activations are prepared once per call (gemv_xprep_kernel)
+        const bool ok_prep = rows > 16 || (nkb * rows + kGemvWaves - 1) / kGemvWaves <= (size_t)kGemvPrepMax;
         if ((ok_lds && ok_prep) || s >= p.kbs) break;
         ++s;
     }
@@ -974,6 +1055,9 @@ GemvPlan gemv_plan(size_t k, size_t n, size_t rows) {
     off += kGemvDummyBytes;
     p.partials_off = off;
     if (s > 1) off += (size_t)p.nbs * s * rows * 128 * 4;
+    off = (off + 255) & ~(size_t)255;
+    p.xpre_off = off;  // rows > 16: prepared activations of up to kGemvMaxTargets matrices
+    if (rows > 16) off += (size_t)kGemvMaxTargets * p.kbs * gemv_frag_bytes_per_kb(rows);
     p.bytes = (off + 255) & ~(size_t)255;
     return p;
 }
@@ -985,16 +1069,22 @@ static hipError_t launch_gemv_kc(const GemvTargets &tg, const void *x, int x_f16
     // x fastest: workgroup (nb, s) is dispatched as nb + s nbs, as a 1-D grid would be
     const dim3 grid((unsigned)p.nbs, (unsigned)p.splits), block(kGemvWaves * 64);
     const int kq = p.kbs / p.splits, kr = p.kbs % p.splits;
-    if (rows > 8)
-        gemv_kernel<K, CB, true><<<grid, block, lds, stream>>>(tg, p.kbs, p.splits, kq, kr, x, x_f16, x_stride,
-                                                               (int)rows, ws + p.dummy_off,
-                                                               (float *)(ws + p.partials_off),
-                                                               (unsigned *)(ws + p.counters_off), y_f16);
-    else
-        gemv_kernel<K, CB, false><<<grid, block, lds, stream>>>(tg, p.kbs, p.splits, kq, kr, x, x_f16, x_stride,
-                                                                (int)rows, ws + p.dummy_off,
-                                                                (float *)(ws + p.partials_off),
-                                                                (unsigned *)(ws + p.counters_off), y_f16);
+    float *part = (float *)(ws + p.partials_off);
+    unsigned *cnt = (unsigned *)(ws + p.counters_off);
+    if (rows > 16) {
+        uint16_t *xp = (uint16_t *)(ws + p.xpre_off);
+        gemv_xprep_kernel<<<dim3((unsigned)((rows + 3) / 4), (unsigned)p.kbs, (unsigned)tg.count), dim3(256), 0,
+                            stream>>>(tg, K, x, x_f16, x_stride, (int)rows, p.kbs, xp);
+        gemv_kernel<K, CB, 2><<<grid, block, lds, stream>>>(tg, p.kbs, p.splits, kq, kr, x, x_f16, x_stride,
+                                                            (int)rows, ws + p.dummy_off, part, cnt, y_f16,
+                                                            (const uint8_t *)xp);
+    } else if (rows > 8) {
+        gemv_kernel<K, CB, 1><<<grid, block, lds, stream>>>(tg, p.kbs, p.splits, kq, kr, x, x_f16, x_stride,
+                                                            (int)rows, ws + p.dummy_off, part, cnt, y_f16, nullptr);
+    } else {
+        gemv_kernel<K, CB, 0><<<grid, block, lds, stream>>>(tg, p.kbs, p.splits, kq, kr, x, x_f16, x_stride,
+                                                            (int)rows, ws + p.dummy_off, part, cnt, y_f16, nullptr);
+    }
     return hipGetLastError();
 }
 

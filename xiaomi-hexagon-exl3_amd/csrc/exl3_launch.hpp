@@ -9,7 +9,9 @@
 
 namespace exl3k {
 
-constexpr int kGemvMaxRows = 16;  // GEMV: hi/lo fp16 halves of 8 rows per 16 MFMA columns, two column blocks
+// GEMV: hi/lo fp16 halves of 8 rows per 16 MFMA columns (one block up to 8 rows, two
+// up to 16); 17..32 rows as two blocks of 16 fp16 rows prepared once per call
+constexpr int kGemvMaxRows = 32;
 constexpr int kGemvWaves = 8;     // waves per GEMV workgroup (a multiple of 4)
 constexpr int kGemmWaves = 4;
 
@@ -48,7 +50,7 @@ struct DecodeBatch {
 
 struct GemvPlan {
     int nbs, kbs, splits, nkw;  // nkw: largest kb count of a split
-    size_t counters_off, dummy_off, partials_off, bytes;
+    size_t counters_off, dummy_off, partials_off, xpre_off, bytes;
 };
 struct GemmPlan {
     int nbs, kbs, bm, mtiles, splits;  // bm: rows per workgroup tile (128 or 256)
