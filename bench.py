@@ -107,9 +107,9 @@ def main():
     rec = torch.from_numpy(synth.pack_records(p, su, sv, BITS).view(np.uint8).copy()).to(dev)
     copies = [rec] + [rec.clone() for _ in range(COPIES - 1)]
     del p
-    xs = {r: torch.from_numpy(synth.activations(1000 + r, r, K_IN)).to(dev) for r in (1, 2, 4, 8, 16)}
+    xs = {r: torch.from_numpy(synth.activations(1000 + r, r, K_IN)).to(dev) for r in (1, 2, 4, 8, 16, 32)}
     x512 = torch.from_numpy(synth.activations(5000, 512, K_IN)).to(dev)
-    row_set = list(range(1, 9)) + [16, 512]
+    row_set = list(range(1, 9)) + [16, 32, 512]
     ys = {r: torch.empty((r, N_OUT), dtype=torch.float16, device=dev) for r in row_set}
     ws = {r: amd.new_workspace(K_IN, N_OUT, r) for r in row_set}
     torch.cuda.synchronize()
@@ -160,7 +160,7 @@ def main():
 
     extra = {}
     if not args.only_gemv:
-        for r in (2, 4, 8, 16):   # 16: the GEMV's largest row count (continuous batching past 8 requests)
+        for r in (2, 4, 8, 16, 32):   # 16, 32: continuous batching past 8 requests (GEMV up to 32 rows)
             ms, _ = timed(r, xs[r], args.steps, args.warmup)
             gbps = algo_bytes(K_IN, N_OUT, BITS, r) / (ms * 1e-3) / 1e9
             extra[f"gemv_rows{r}"] = {"gbps": round(gbps, 1), "kernel_us": round(ms * 1e3, 2),
@@ -223,7 +223,7 @@ def main():
                    "k": K_IN, "n": N_OUT, "bits": BITS, "rows": 1, "weight_copies": COPIES},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "kernel": "exl3k::gemv_kernel<4,2,false>", "kernel_us_mean": round(ms1 * 1e3, 3),
+                     "kernel": "exl3k::gemv_kernel<4,2,0>", "kernel_us_mean": round(ms1 * 1e3, 3),
                      "algorithmic_bytes": b1},
         "cpu_baseline": cpu,
     }

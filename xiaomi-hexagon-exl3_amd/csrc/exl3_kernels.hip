@@ -1,13 +1,13 @@
 // exl3_kernels.hip -- gfx950 kernels of the EXL3 packed-weight linear layer.
 //
-//   gemv_kernel      rows 1..16: each lane decodes 16 trellis positions of a tile
+//   gemv_kernel      rows 1..32: each lane decodes 16 trellis positions of a tile
 //                    straight into an fp16 MFMA A-fragment (W^T), the activations
 //                    H128(x*su) arrive pre-split into fp16 hi/lo halves in the 16
 //                    MFMA columns, v_mfma_f32_16x16x32_f16 accumulates in fp32;
 //                    split-K partials are reduced in fixed order by the last
 //                    workgroup of each 128-column group, which applies H128 and sv.
 //   gemm_xprep_kernel, gemm_kernel, gemm_reduce_kernel
-//                    rows > 16: H128(x*su) once in fp16 MFMA-fragment order; a
+//                    rows > 32: H128(x*su) once in fp16 MFMA-fragment order; a
 //                    workgroup (k split, column group, m-tile) decodes record kb + 1
 //                    into LDS (fp16, swizzled) while v_mfma_f32_32x32x16_f16 runs on
 //                    record kb, fp32 accumulation; split partials are summed in
@@ -1230,7 +1230,7 @@ __global__ __launch_bounds__(256) void gemm_xprep_kernel(const uint8_t *__restri
     }
 }
 
-// GEMM (rows > 16).  Workgroup (split s, m-tile mt, column group nb): rows
+// GEMM (rows > 32).  Workgroup (split s, m-tile mt, column group nb): rows
 // [BM mt, +BM) x columns [128 nb, +128), records kb in [kb0, kb1); BM = 64 RB
 // rows, wave w owning rows 32 RB w .. +32 RB for all 128 columns: RB x 4
 // accumulator blocks of v_mfma_f32_32x32x16_f16 (one wave per SIMD keeps this

@@ -168,7 +168,7 @@ class _MatrixDesc(ctypes.Structure):
 
 def mul_mat_group(mats, bits, k, x, codebook=CB_MUL1, out_dtype=None, workspace=None, stream=None):
     """[y_i] = layer_i(x) for matrices [(records_i, n_i)] (or (records_i, n_i, y_i)) sharing k, bits, codebook
-    and x: one launch at rows <= 16 (exl3_hip_gemv_max_rows)."""
+    and x: one GEMV launch at rows <= exl3_hip_gemv_max_rows() (32)."""
     import torch
     assert x.dim() == 2 and x.stride(1) == 1 and x.dtype in (torch.float16, torch.float32)
     rows = x.shape[0]
