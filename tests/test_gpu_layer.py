@@ -174,7 +174,7 @@ def test_linearity_full_size(amd):
         assert_layer_close(ys[2], ys[0] + ys[1], what=f"linearity rows={rows}")
 
 
-@pytest.mark.parametrize("rows", [1, 5, 14, 37])
+@pytest.mark.parametrize("rows", [1, 5, 14, 24, 37])
 def test_graph_replay_matches_eager(amd, oracle, rows):
     """A HIP graph of mul_mat calls (split-K counters self-reset, no memset
     nodes) replays bit-identically, with eager work between the replays."""
