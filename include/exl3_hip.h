@@ -23,7 +23,7 @@
  *                            tied embedding exl3::Model::embedding src/exl3_model.cpp:168-187
  *   exl3_hip_codebook     <- exl3::decode_codebook      src/exl3_codec.cpp:68-86
  *   exl3_hip_hadamard128  <- exl3::hadamard128          src/exl3_codec.cpp:147-167
- *   exl3_hip_pack_records <- record assembly tests/test-exl3-graph.cpp:110-118,
+ *   exl3_hip_pack_records <- record assembly tests/test-exl3-graph.cpp:37-45,
  *                            tools/export_native_gguf.py:27-36
  *   exl3_hip_validate_records <- ggml_validate_row_data EXL3 case
  *                            patches/llama-exl3.patch:327-338
@@ -78,8 +78,9 @@ int exl3_hip_supports_mul_mat(unsigned bits, unsigned codebook, size_t k, size_t
  * 1..rows.  The workspace holds per-call staging and self-resetting completion
  * counters: zero-fill it once before its first use (exl3_hip_workspace_init).
  * One workspace serves any sequence of calls whose n agree, or all stay
- * <= 65536, and whose k and rows it was sized for; calls that share one must
- * not run concurrently (order them on one stream). */
+ * <= 65536, when it holds at least exl3_hip_mul_mat_workspace_bytes(k, n, rows)
+ * of every one of them; calls that share one must not run concurrently (order
+ * them on one stream). */
 size_t exl3_hip_mul_mat_workspace_bytes(size_t k, size_t n, size_t rows);
 exl3_status exl3_hip_workspace_init(void *workspace, size_t workspace_bytes, hipStream_t stream);
 
@@ -93,7 +94,12 @@ exl3_status exl3_hip_workspace_init(void *workspace, size_t workspace_bytes, hip
  *   y            device, rows x n of yt, row stride y_row_stride elements (>= n)
  *   workspace    device, >= exl3_hip_mul_mat_workspace_bytes(k, n, rows), zero-filled
  *                before first use; NULL -> an internal per-(device, stream)
- *                workspace is allocated on first use and kept
+ *                workspace is allocated on first use and kept (grown, never
+ *                freed, when a larger call needs more).  While the stream is
+ *                being captured into a HIP graph the internal workspace cannot
+ *                grow: such a call returns EXL3_WORKSPACE_TOO_SMALL unless an
+ *                uncaptured call of at least this size came first; callers that
+ *                capture should pass their own workspace
  * Deterministic: the same inputs give the same bits on every call.
  */
 exl3_status exl3_hip_mul_mat(const void *records, unsigned bits, unsigned codebook, size_t k, size_t n,

@@ -323,7 +323,7 @@ static size_t record_offset(size_t nb, size_t kb, size_t k, unsigned bits)
     return (nb * (k / 128) + kb) * orc_group_bytes(bits);
 }
 
-/* tests/test-exl3-graph.cpp:110-118, tools/export_native_gguf.py:27-36:
+/* tests/test-exl3-graph.cpp:37-45, tools/export_native_gguf.py:27-36:
  * record (nb, kb), tile (r, c) = upstream tile (8 kb + r, 8 nb + c) */
 int orc_pack_records(const uint16_t *packed, const uint16_t *su, const uint16_t *sv, size_t k,
                      size_t n, unsigned bits, void *records)

@@ -64,7 +64,7 @@ int orc_get_rows(const void *records, unsigned bits, unsigned cb, size_t k, size
                  size_t count, float *out, size_t out_stride);
 size_t orc_group_bytes(unsigned bits); /* include/exl3-block.h:14 */
 
-/* upstream tiles + su + sv -> records, tests/test-exl3-graph.cpp:110-118 and
+/* upstream tiles + su + sv -> records, tests/test-exl3-graph.cpp:37-45 and
  * tools/export_native_gguf.py:27-36 */
 int orc_pack_records(const uint16_t *packed, const uint16_t *su, const uint16_t *sv, size_t k,
                      size_t n, unsigned bits, void *records);

@@ -60,7 +60,7 @@ def activations(seed, rows, k, sigma=1.0):
 
 def pack_records(packed, su, sv, bits):
     """Upstream tiles + scales -> 128x128 group records (bytes), the layout of
-    include/exl3-block.h; tests/test-exl3-graph.cpp:110-118."""
+    include/exl3-block.h; tests/test-exl3-graph.cpp:37-45."""
     kt, nt, w = packed.shape
     k, n = kt * 16, nt * 16
     assert w == 16 * bits and k % 128 == 0 and n % 128 == 0

@@ -125,6 +125,21 @@ def test_cpp_codec_api_program():
     assert r.returncode == 0 and "PASS" in r.stdout
 
 
+REF_TEST_ON_HIP = Path(__file__).resolve().parents[1] / "oracle" / "_ref" / "test_codec_hip"
+
+
+@pytest.mark.skipif(not REF_TEST_ON_HIP.exists(), reason="built only where the reference checkout was present")
+def test_reference_codec_test_on_hip_library():
+    """The reference's own codec test (tests/test_codec.cpp), compiled against
+    this repository's include/ (exl3_codec.h, exl3-block.h) and linked with
+    libexl3_hip.so by oracle/Makefile: its mul1 closed form, fp16 rounding,
+    H128 involution, zero ring, rejections and VTCM planner checks all pass
+    against the GPU-backed codec."""
+    r = subprocess.run([str(REF_TEST_ON_HIP)], capture_output=True, text=True, timeout=300)
+    print(r.stdout, r.stderr, flush=True)
+    assert r.returncode == 0 and r.stdout.startswith("PASS"), r.stdout + r.stderr
+
+
 def test_decode_batch_matches_single_decodes(amd, oracle):
     """exl3_hip_decode_batch: 45 matrices of every rate (more than one launch's
     32 for 4 bits), upstream tiles, each bit-identical with its own

@@ -281,3 +281,76 @@ def test_concurrent_streams(amd):
             for i in range(2):
                 for j, r in enumerate(row_counts):
                     assert torch.equal(outs[i][j], ref[i][j]), f"stream {i} rows={r} rep={rep} ws={use_ws}"
+
+
+def test_one_workspace_serves_mixed_widths(amd):
+    """One caller workspace shared by layers of different n (all <= 65536) and
+    both kernels: a GEMM call at n=2048 (its activation staging sits behind the
+    counter region), then GEMV calls at n=14336 (more column groups, so more
+    counters) and a gate/up group (n = 2 x 6144).  The counter region does not
+    depend on n, so no call writes over another's counters: every result equals
+    the one from a fresh workspace, over two rounds of the sequence."""
+    import torch
+    cases = {  # name: (k, [n...], rows, bits)
+        "gemm_n2048": (4096, [2048], 64, 4),
+        "gemv_n14336": (4096, [14336], 1, 4),
+        "gemv_n14336_r8": (4096, [14336], 8, 4),
+        "group_gate_up": (4096, [6144, 6144], 3, 4),
+        "gemv_n2048_r24": (4096, [2048], 24, 4),
+    }
+    recs = {name: [dev(make_layer(950 + 7 * i + j, k, n, bits)) for j, n in enumerate(ns)]
+            for i, (name, (k, ns, rows, bits)) in enumerate(cases.items())}
+    xs = {name: torch.from_numpy(synth.activations(970 + i, rows, k)).cuda()
+          for i, (name, (k, ns, rows, bits)) in enumerate(cases.items())}
+
+    def call(name, ws):
+        k, ns, rows, bits = cases[name]
+        if len(ns) > 1:
+            return [y.clone() for y in amd.mul_mat_group([(r, n) for r, n in zip(recs[name], ns)], bits, k, xs[name],
+                                                         workspace=ws)]
+        return [amd.mul_mat(recs[name][0], bits, k, ns[0], xs[name], workspace=ws).clone()]
+
+    fresh = {}
+    for name, (k, ns, rows, bits) in cases.items():
+        fresh[name] = call(name, amd.new_workspace(k, sum(ns), rows))
+    torch.cuda.synchronize()
+    size = max(amd.workspace_bytes(k, sum(ns), rows) for k, ns, rows, _ in cases.values())
+    shared = torch.zeros(size, dtype=torch.uint8, device="cuda")
+    for rnd in range(2):
+        for name in ("gemm_n2048", "gemv_n14336", "group_gate_up", "gemm_n2048", "gemv_n14336_r8",
+                     "gemv_n2048_r24", "gemv_n14336", "group_gate_up"):
+            got = call(name, shared)
+            torch.cuda.synchronize()
+            for a, b in zip(got, fresh[name]):
+                assert torch.equal(a, b), f"round {rnd}: {name} differs from a fresh workspace"
+
+
+def test_internal_workspace_under_capture(amd):
+    """With no caller workspace, a call captured into a HIP graph before any
+    uncaptured call of its size is refused with EXL3_WORKSPACE_TOO_SMALL (the
+    internal workspace cannot grow during capture) instead of allocating; after
+    one uncaptured call the same capture succeeds and replays equal eager calls."""
+    import torch
+    k, n, bits, rows = 1024, 640, 4, 2   # a shape no other test uses: its internal workspace is new
+    rd = dev(make_layer(990, k, n, bits))
+    x = torch.from_numpy(synth.activations(991, rows, k)).cuda()
+    y = torch.empty((rows, n), dtype=torch.float16, device="cuda")
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with pytest.raises(amd.Exl3Error) as err:
+        with torch.cuda.graph(g, stream=s):
+            amd.mul_mat(rd, bits, k, n, x, y=y, stream=s)
+    assert err.value.status == amd.WORKSPACE_TOO_SMALL
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        eager = amd.mul_mat(rd, bits, k, n, x, stream=s).clone()   # grows the internal workspace
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        amd.mul_mat(rd, bits, k, n, x, y=y, stream=s)
+    for _ in range(3):
+        y.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager)

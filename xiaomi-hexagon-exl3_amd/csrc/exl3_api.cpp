@@ -11,6 +11,7 @@
 #include <algorithm>
 #include <tuple>
 #include <utility>
+#include <vector>
 
 #include "exl3_launch.hpp"
 
@@ -32,13 +33,19 @@ bool valid_matrix(size_t k, size_t n, size_t multiple) {
 
 // Internal workspaces, one per (device, stream, counter-region size), grown on
 // demand, zero-filled when created and kept until process exit.  Calls that
-// share one have the same counter layout (exl3k::counter_region_bytes).
+// share one have the same counter layout (exl3k::counter_region_bytes).  A
+// workspace that is outgrown is retired, never freed: a call on another thread
+// may still be enqueuing kernels that use it.  Growth allocates, so it is
+// refused while the stream is being captured into a HIP graph: a caller that
+// captures passes its own workspace, or makes one uncaptured call of the
+// largest shape first.
 struct InternalWs {
     void *ptr = nullptr;
     size_t bytes = 0;
 };
 std::mutex g_ws_mutex;
 std::map<std::tuple<int, hipStream_t, size_t>, InternalWs> g_ws;
+std::vector<void *> g_ws_retired;
 
 exl3_status internal_workspace(size_t need, size_t n, hipStream_t stream, void **out) {
     int dev = 0;
@@ -46,20 +53,19 @@ exl3_status internal_workspace(size_t need, size_t n, hipStream_t stream, void *
     std::lock_guard<std::mutex> lock(g_ws_mutex);
     InternalWs &ws = g_ws[std::make_tuple(dev, stream, exl3k::counter_region_bytes(n))];
     if (ws.bytes < need) {
-        if (ws.ptr) {
-            if (hipStreamSynchronize(stream) != hipSuccess) return EXL3_HIP_ERROR;
-            (void)hipFree(ws.ptr);
-            ws.ptr = nullptr;
-            ws.bytes = 0;
-        }
+        hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(stream, &capture) != hipSuccess) return EXL3_HIP_ERROR;
+        if (capture != hipStreamCaptureStatusNone) return EXL3_WORKSPACE_TOO_SMALL;
+        const size_t bytes = std::max(need, 2 * ws.bytes);  // geometric growth bounds what is retired
         void *p = nullptr;
-        if (hipMalloc(&p, need) != hipSuccess) return EXL3_HIP_ERROR;
-        if (exl3k::launch_zero(p, need, stream) != hipSuccess) {
+        if (hipMalloc(&p, bytes) != hipSuccess) return EXL3_HIP_ERROR;
+        if (exl3k::launch_zero(p, bytes, stream) != hipSuccess) {
             (void)hipFree(p);
             return EXL3_HIP_ERROR;
         }
+        if (ws.ptr) g_ws_retired.push_back(ws.ptr);
         ws.ptr = p;
-        ws.bytes = need;
+        ws.bytes = bytes;
     }
     *out = ws.ptr;
     return EXL3_OK;

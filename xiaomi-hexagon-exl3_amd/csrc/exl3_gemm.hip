@@ -1,0 +1,579 @@
+// exl3_gemm.hip -- the EXL3 layer at rows > 32 on gfx950 (gemm_xprep_kernel,
+// gemm_kernel, gemm_reduce_kernel): H128(x*su) once in fp16 MFMA-fragment order;
+// a workgroup (k split, column group, m-tile) decodes record kb + 1 into LDS
+// (fp16, swizzled) while v_mfma_f32_32x32x16_f16 runs on record kb, fp32
+// accumulation; split partials are summed in fixed order by the reduce kernel,
+// which applies H128 and sv.
+// Reference semantics: src/exl3-ggml.cpp:51-92.
+#include <hip/hip_runtime.h>
+
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "exl3_kernel_common.hpp"
+
+namespace exl3k {
+
+// ============================================================== GEMM
+// Activation prep for the GEMM: xh = fp16(H128(x[r] * su)) (su from record
+// (0, kb), src/exl3-ggml.cpp:60-73), rows padded with zeros to the tile height,
+// stored in MFMA A-fragment order so that the GEMM loads one fragment as one
+// contiguous kilobyte: block (rows 32 rb .. +31, k 128 kb + 16 ks .. +15) is 64
+// lanes x 8 halves, lane l = row % 32 + 32 (k % 16 / 8), element k % 8; blocks
+// ordered (rb, kb, ks), so (rb, kb) is one contiguous 8 KB run.
+__host__ __device__ inline size_t gemm_xh_offset(int row, int kb, int e, int kbs) {  // halves
+    const int ks = e >> 4, kk = e & 15;
+    const int ln = (row & 31) + 32 * (kk >> 3);
+    return ((((size_t)(row >> 5) * kbs + kb) * 8 + ks) * 64 + ln) * 8 + (kk & 7);
+}
+// Workgroup (kb, rb), 4 waves x 8 rows (two passes of 4); lane 16 g + l holds
+// elements 8 i .. 8 i + 7, i = h128_lane_block(l), of row 32 rb + 8 wave + 4 pass
+// + g.  H128 stages 1, 2 and 4 are inside the lane, 8 .. 64 pair it with the
+// lanes holding i ^ 1 .. 8 (one DPP read each); the lane's eight results are one
+// 16-byte unit of the fragment layout, stored directly.
+template <bool XF16>
+__device__ __forceinline__ void xprep_load(const void *__restrict__ x, const size_t (&off)[2], float (&v)[2][8]) {
+#pragma unroll
+    for (int ps = 0; ps < 2; ++ps) {
+        if constexpr (XF16) {
+            const uint16_t *p = (const uint16_t *)x + off[ps];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[ps][j] = half_bits_to_float(p[j]);
+        } else {
+            const float *p = (const float *)x + off[ps];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[ps][j] = p[j];
+        }
+    }
+}
+__global__ __launch_bounds__(256) void gemm_xprep_kernel(const uint8_t *__restrict__ records, int bits,
+                                                         const void *__restrict__ x, int x_f16, size_t x_stride,
+                                                         int rows, int kbs, uint16_t *__restrict__ xh16) {
+    // i: this lane's 8-element block of the row (h128_lane_block order)
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, i = h128_lane_block(lane & 15);
+    const int kb = blockIdx.x, rb = blockIdx.y;
+    const size_t col = (size_t)kb * 128 + 8 * i;
+    const uint4 su8 = *(const uint4 *)(records + (size_t)kb * group_bytes(bits) + 2048 * bits + 16 * i);
+    const uint32_t suw[4] = {su8.x, su8.y, su8.z, su8.w};
+    float v[2][8];
+    size_t off[2];  // rows past the end read row 0
+#pragma unroll
+    for (int ps = 0; ps < 2; ++ps) {
+        const int r = 32 * rb + 8 * wave + 4 * ps + g;
+        off[ps] = (size_t)(r < rows ? r : 0) * x_stride + col;
+    }
+    if (x_f16) xprep_load<true>(x, off, v);  // all loads before the first use
+    else xprep_load<false>(x, off, v);
+    // stage-major over the 16 values of both passes: independent DPP reads and
+    // butterflies back to back, no wait states between a write and its DPP read
+#pragma unroll
+    for (int ps = 0; ps < 2; ++ps) {
+        const int r = 32 * rb + 8 * wave + 4 * ps + g;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            v[ps][j] = r < rows ? v[ps][j] * half_bits_to_float((uint16_t)(suw[j >> 1] >> (16 * (j & 1)))) : 0.f;
+    }
+#pragma unroll
+    for (int st = 1; st < 8; st <<= 1)
+#pragma unroll
+        for (int ps = 0; ps < 2; ++ps)
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (!(j & st)) {
+                    const float a = v[ps][j], b = v[ps][j | st];
+                    v[ps][j] = a + b;
+                    v[ps][j | st] = a - b;
+                }
+    auto lane_stage = [&](auto sc) {
+        constexpr int S = decltype(sc)::value;
+        const float sgn = (i & S) ? -1.f : 1.f;
+        float p[2][8];
+#pragma unroll
+        for (int ps = 0; ps < 2; ++ps)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) p[ps][j] = dpp_block_xor<S>(v[ps][j]);
+#pragma unroll
+        for (int ps = 0; ps < 2; ++ps)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[ps][j] = __builtin_fmaf(v[ps][j], sgn, p[ps][j]);
+    };
+    lane_stage(std::integral_constant<int, 1>{});
+    lane_stage(std::integral_constant<int, 2>{});
+    lane_stage(std::integral_constant<int, 4>{});
+    lane_stage(std::integral_constant<int, 8>{});
+#pragma unroll
+    for (int ps = 0; ps < 2; ++ps) {
+        const int r = 32 * rb + 8 * wave + 4 * ps + g;
+        float e[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) e[j] = v[ps][j] * 0.08838834764831844055f;
+        uint4 out;
+        out.x = (uint32_t)float_to_half_bits(e[0]) | ((uint32_t)float_to_half_bits(e[1]) << 16);
+        out.y = (uint32_t)float_to_half_bits(e[2]) | ((uint32_t)float_to_half_bits(e[3]) << 16);
+        out.z = (uint32_t)float_to_half_bits(e[4]) | ((uint32_t)float_to_half_bits(e[5]) << 16);
+        out.w = (uint32_t)float_to_half_bits(e[6]) | ((uint32_t)float_to_half_bits(e[7]) << 16);
+        *(uint4 *)(xh16 + gemm_xh_offset(r, kb, 8 * i, kbs)) = out;
+    }
+}
+
+// GEMM (rows > 32).  Workgroup (split s, m-tile mt, column group nb): rows
+// [BM mt, +BM) x columns [128 nb, +128), records kb in [kb0, kb1); BM = 64 RB
+// rows, wave w owning rows 32 RB w .. +32 RB for all 128 columns: RB x 4
+// accumulator blocks of v_mfma_f32_32x32x16_f16 (one wave per SIMD keeps this
+// MFMA at full rate; the 16x16 one needs two).  Per record kb, software-pipelined
+// in straight-line code per k-step (16 k):
+//   * MFMAs of k-step ks (A = activations, B = decoded weights), the B fragments
+//     of k-step ks + 1 already being read from LDS;
+//   * one eighth of the decode of record kb + 1 (fragment ks / 2 of the wave's
+//     chunk ks % 2: the GEMV's chunk decoder) into the other LDS buffer W[n][k]
+//     (fp16, 16-byte k-chunks XOR-swizzled by n % 16: conflict-free MFMA B
+//     reads), interleaved with the MFMAs;
+//   * the activations of k-step ks of record kb + 1 (xh16, fragment-tiled and
+//     L2-resident: every column group reads it), into the registers just consumed.
+// The weight words are loaded two records ahead.  MFMA 32x32x16 operands: A lane l
+// = row l % 32, k 8 (l / 32) + j; B lane l = column l % 32, k 8 (l / 32) + j;
+// D element e of lane l = row (e % 4) + 8 (e / 4) + 4 (l / 32), column l % 32.
+// Split-K partials (kept in the accumulator layout) are summed in split order by
+// the last workgroup of the tile, which applies H128 over the 128 columns of
+// each row in registers (strides 1..16: lanes, 32 and 64: blocks) and sv
+// (src/exl3-ggml.cpp:84-90).
+constexpr int kGemmTargetWgs = 256;  // one 4-wave workgroup per CU (the accumulators fill the register file)
+
+__device__ __forceinline__ int gemm_w_offset(int n, int chunk) {  // halves
+    return n * 128 + ((chunk ^ (n & 15)) << 3);
+}
+
+
+// Output of accumulator values in the 32x32 MFMA D layout: t[cb][i] is column
+// 32 cb + lane % 32 of row row0 + (i % 4) + 8 (i / 4) + 4 (lane / 32).  H128 over
+// the 128 columns of each row in natural stage order (strides 1..16 pair lanes
+// lane ^ 1..16 by DPP and v_permlane16_swap, strides 32 and 64 pair blocks cb ^ 1, 2;
+// src/exl3_codec.cpp:153-165),
+// then 1/sqrt(128) and sv (src/exl3-ggml.cpp:84-90).
+template <int NE>
+__device__ __forceinline__ void gemm_rows_out(float (&t)[4][NE], int lane, int row0, const uint16_t *svp, int rows,
+                                              void *y, int y_f16, size_t y_stride, size_t col0, const void *res,
+                                              size_t res_stride) {
+    const int l32 = lane & 31, lh = lane >> 5;
+    // lane stages stage-major over the 4 NE independent values: the DPP reads
+    // and butterflies of one stage issue back to back without wait states
+    auto lane_stage = [&](auto sc) {
+        constexpr int S = decltype(sc)::value;
+        if constexpr (S == 16) {  // v_permlane16_swap (lane_butterfly): VALU, no LDS round trip
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+                for (int i = 0; i < NE; ++i) t[cb][i] = lane_butterfly<16>(t[cb][i], l32);
+        } else {
+            const float sgn = (l32 & S) ? -1.f : 1.f;
+            float p[4][NE];
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+                for (int i = 0; i < NE; ++i) p[cb][i] = dpp_xor<S>(t[cb][i]);
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+                for (int i = 0; i < NE; ++i) t[cb][i] = __builtin_fmaf(t[cb][i], sgn, p[cb][i]);
+        }
+    };
+    lane_stage(std::integral_constant<int, 1>{});
+    lane_stage(std::integral_constant<int, 2>{});
+    lane_stage(std::integral_constant<int, 4>{});
+    lane_stage(std::integral_constant<int, 8>{});
+    lane_stage(std::integral_constant<int, 16>{});
+#pragma unroll
+    for (int st = 1; st < 4; st <<= 1)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+            if (!(cb & st))
+#pragma unroll
+                for (int i = 0; i < NE; ++i) {
+                    const float a = t[cb][i], b = t[cb | st][i];
+                    t[cb][i] = a + b;
+                    t[cb | st][i] = a - b;
+                }
+    float svv[4];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) svv[cb] = half_bits_to_float(svp[32 * cb + l32]);
+    // res (y's dtype): y = res + layer with one rounding of the sum
+    auto store = [&](auto is_f16, auto has_res) {
+        constexpr bool YF16 = decltype(is_f16)::value, RES = decltype(has_res)::value;
+        typedef typename std::conditional<YF16, uint16_t, float>::type T;
+#pragma unroll
+        for (int i = 0; i < NE; ++i) {
+            const int row = row0 + (i & 3) + 8 * (i >> 2) + 4 * lh;
+            if (row < rows) {
+                T *yr = (T *)y + (size_t)row * y_stride + col0 + l32;
+                const T *rr = (const T *)res + (size_t)row * res_stride + col0 + l32;
+#pragma unroll
+                for (int cb = 0; cb < 4; ++cb) {
+                    float v = t[cb][i] * 0.08838834764831844055f * svv[cb];
+                    if constexpr (RES) {
+                        if constexpr (YF16) v += half_bits_to_float(rr[32 * cb]);
+                        else v += rr[32 * cb];
+                    }
+                    if constexpr (YF16) yr[32 * cb] = float_to_half_bits(v);
+                    else yr[32 * cb] = v;
+                }
+            }
+        }
+    };
+    if (res) {
+        if (y_f16) store(std::true_type{}, std::true_type{});
+        else store(std::false_type{}, std::true_type{});
+    } else {
+        if (y_f16) store(std::true_type{}, std::false_type{});
+        else store(std::false_type{}, std::false_type{});
+    }
+}
+
+template <int K, int CB, int RB>
+__global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
+    const uint8_t *__restrict__ records, int kbs, int nbs, int mtiles, int splits, int kq, int kr,
+    const uint16_t *__restrict__ xh16, size_t k, uint16_t *__restrict__ partials, void *y, int y_f16, size_t y_stride,
+    int rows, const void *res, size_t res_stride) {
+    constexpr int BM = 32 * RB * kGemmWaves;
+    constexpr size_t GB = (size_t)2048 * K + 512;
+    __shared__ __attribute__((aligned(16))) uint16_t wlds[2][128 * 128];  // 64 KB
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lg = lane >> 4, li = lane & 15, j = li & 7;
+    const int l32 = lane & 31, lh = lane >> 5;
+    // Workgroups are dispatched to the 8 XCDs round-robin (blockIdx % 8) and each
+    // XCD has its own L2: renumber so that XCD x runs the contiguous range
+    // [x G / 8, (x + 1) G / 8) of the order (split, column group, m-tile), m-tile
+    // fastest.  The m-tiles of one column group then share its weight records,
+    // and the column groups of one split share its activation rows, in one L2.
+    const int G = gridDim.x;
+    int L = (G & 7) ? (int)blockIdx.x : (int)(blockIdx.x & 7) * (G >> 3) + (int)(blockIdx.x >> 3);
+    const int s = L / (mtiles * nbs);
+    L -= s * mtiles * nbs;
+    const int nb = L / mtiles, mt = L - nb * mtiles;
+    const int tile = mt * nbs + nb;
+    // split s owns kq + (s < kr) records from kb0 (kq = kbs / splits, kr = kbs % splits, from the host)
+    const int kb0 = s * kq + (s < kr ? s : kr), kb1 = kb0 + kq + (s < kr ? 1 : 0);
+    const uint8_t *colgroup = records + (size_t)nb * kbs * GB;
+
+    // weights: this wave decodes groups q = 2 wave + h (h = 0, 1) of every record
+    uint32_t wlane[2];
+    int wn0[2], wc0[2];  // column and k-chunk of fragment 0 of each chunk
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int q = 2 * wave + h, r4 = q >> 2, c2 = q & 3;
+        wlane[h] = (uint32_t)(r4 * 1024 * K + ((8 * lg + 2 * c2 + (li >> 3)) * 32 + 4 * j) * K);
+        wn0[h] = 16 * (2 * c2 + (li >> 3)) + j;
+        wc0[h] = 2 * (4 * r4 + lg);
+    }
+    auto load_words = [&](int kb, uint32_t (&w)[2][K]) {
+        const uint8_t *rec = colgroup + (size_t)(kb < kb1 ? kb : kb1 - 1) * GB;  // past the end: re-read, unused
+        load_chunk<K>(rec + wlane[0], w[0]);
+        load_chunk<K>(rec + wlane[1], w[1]);
+    };
+    const bool first_chunk = j == 0;
+    // boundary words of the two chunks (see decode_chunk), for the pieces below
+    auto chunk_prepare = [&](const uint32_t (&w)[2][K], uint32_t (&xb)[2][K]) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t p1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)w[h][K - 1], 0x121, 0xF, 0xF, false);
+            const uint32_t p9 = (uint32_t)__builtin_amdgcn_mov_dpp((int)w[h][K - 1], 0x129, 0xF, 0xF, false);
+            xb[h][0] = __builtin_amdgcn_alignbit(first_chunk ? p9 : p1, w[h][0], 16);
+#pragma unroll
+            for (int m = 1; m < K; ++m) xb[h][m] = __builtin_amdgcn_alignbit(w[h][m - 1], w[h][m], 16);
+        }
+    };
+    // piece P: fragment F = P / 2 of chunk h = P % 2 -> LDS at column
+    // n0 + 8 (F >> 1), k-chunk c0 + (F & 1)
+    auto decode_piece = [&](auto pc, const uint32_t (&w)[2][K], const uint32_t (&xb)[2][K], uint16_t *dst) {
+        constexpr int F = decltype(pc)::value >> 1, h = decltype(pc)::value & 1;
+        const u4 fr = chunk_frag<K, CB, F>(w[h], xb[h]);
+        *(u4 *)(dst + gemm_w_offset(wn0[h] + 8 * (F >> 1), wc0[h] + (F & 1))) = fr;
+    };
+    // activations: A fragment (ks, rb) = the contiguous kilobyte of row block
+    // (BM mt + 32 (RB wave + rb)) / 32, record kb, k-step ks (gemm_xh_offset)
+    const uint16_t *xblk = xh16 + ((size_t)(mt * BM / 32 + RB * wave) * kbs * 8 * 64 + lane) * 8;
+    auto load_x_step = [&](int kb, int ks, h8 (&xs)[RB]) {
+        const uint16_t *p = xblk + ((size_t)(kb < kb1 ? kb : kb1 - 1) * 8 + ks) * 512;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) xs[rb] = *(const h8 *)(p + (size_t)rb * kbs * 8 * 512);
+    };
+    // B fragment (ks, cb): column 32 cb + l32, k-chunk 2 ks + lh; the swizzle term
+    // depends on the lane and k-step only, so the four blocks sit at constant
+    // offsets from one address
+    auto read_b = [&](const uint16_t *wsrc, int ks, h8 (&b)[4]) {
+        const uint16_t *base = wsrc + l32 * 128 + (((2 * ks + lh) ^ li) << 3);
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) b[cb] = *(const h8 *)(base + cb * 32 * 128);
+    };
+
+    f16v acc[RB][4];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[rb][cb][e] = 0.f;
+    auto mma_step = [&](const h8 (&xs)[RB], const h8 (&b)[4]) {
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+                acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xs[rb], b[cb], acc[rb][cb], 0, 0, 0);
+    };
+
+    // prologue: words of kb0 and kb0 + 1, activations of kb0, record kb0 decoded,
+    // B fragments of its first k-step
+    uint32_t wbuf[2][2][K], xb[2][K];
+    h8 xa[8][RB];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) load_x_step(kb0, ks, xa[ks]);
+    load_words(kb0, wbuf[0]);
+    load_words(kb0 + 1, wbuf[1]);
+    chunk_prepare(wbuf[0], xb);
+    decode_piece(std::integral_constant<int, 0>{}, wbuf[0], xb, wlds[0]);
+    decode_piece(std::integral_constant<int, 1>{}, wbuf[0], xb, wlds[0]);
+    decode_piece(std::integral_constant<int, 2>{}, wbuf[0], xb, wlds[0]);
+    decode_piece(std::integral_constant<int, 3>{}, wbuf[0], xb, wlds[0]);
+    decode_piece(std::integral_constant<int, 4>{}, wbuf[0], xb, wlds[0]);
+    decode_piece(std::integral_constant<int, 5>{}, wbuf[0], xb, wlds[0]);
+    decode_piece(std::integral_constant<int, 6>{}, wbuf[0], xb, wlds[0]);
+    decode_piece(std::integral_constant<int, 7>{}, wbuf[0], xb, wlds[0]);
+    __syncthreads();
+    h8 bc[4], bn[4];
+    read_b(wlds[0], 0, bc);
+
+    // one k-step: B of ks + 1 requested, MFMAs of ks, a decode piece, then the
+    // activations of ks for the next record
+    auto kstep = [&](auto kc, int kb, const uint16_t *wcur, uint16_t *wnext, const uint32_t (&wnextw)[2][K],
+                     h8 (&bcur)[4], h8 (&bnxt)[4]) {
+        constexpr int KS = decltype(kc)::value;
+        if constexpr (KS < 7) read_b(wcur, KS + 1, bnxt);
+        mma_step(xa[KS], bcur);
+        decode_piece(std::integral_constant<int, KS>{}, wnextw, xb, wnext);
+        load_x_step(kb + 1, KS, xa[KS]);
+        // One MFMA every few VALU instructions: the wave issues in order, so
+        // MFMAs back to back stall it while the decode waits behind them.  The
+        // B reads lead, the activation loads (seven k-steps ahead of their use:
+        // left alone the scheduler sinks them to the end of the record) trail.
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            if (i < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+            __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
+            if (i == 7) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
+            if (i >= 6) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // record kb: activations xa, decoded weights wcur (B fragments of k-step 0 in
+    // bc); words of kb + 1 in wnextw; slot wfree takes the words of kb + 2
+    auto step = [&](int kb, const uint16_t *wcur, uint16_t *wnext, uint32_t (&wfree)[2][K],
+                    const uint32_t (&wnextw)[2][K]) {
+        load_words(kb + 2, wfree);
+        chunk_prepare(wnextw, xb);
+        kstep(std::integral_constant<int, 0>{}, kb, wcur, wnext, wnextw, bc, bn);
+        kstep(std::integral_constant<int, 1>{}, kb, wcur, wnext, wnextw, bn, bc);
+        kstep(std::integral_constant<int, 2>{}, kb, wcur, wnext, wnextw, bc, bn);
+        kstep(std::integral_constant<int, 3>{}, kb, wcur, wnext, wnextw, bn, bc);
+        kstep(std::integral_constant<int, 4>{}, kb, wcur, wnext, wnextw, bc, bn);
+        kstep(std::integral_constant<int, 5>{}, kb, wcur, wnext, wnextw, bn, bc);
+        kstep(std::integral_constant<int, 6>{}, kb, wcur, wnext, wnextw, bc, bn);
+        kstep(std::integral_constant<int, 7>{}, kb, wcur, wnext, wnextw, bn, bc);
+        __syncthreads();  // wnext complete; every wave is done reading wcur
+        read_b(wnext, 0, bc);
+    };
+    int kb = kb0;
+    for (; kb + 2 <= kb1; kb += 2) {
+        step(kb, wlds[0], wlds[1], wbuf[0], wbuf[1]);
+        step(kb + 1, wlds[1], wlds[0], wbuf[1], wbuf[0]);
+    }
+    if (kb < kb1) {  // odd count: the last record is in wlds[0]
+#pragma unroll
+        for (int ks = 0; ks < 8; ks += 2) {
+            read_b(wlds[0], ks + 1, bn);
+            mma_step(xa[ks], bc);
+            if (ks + 2 < 8) read_b(wlds[0], ks + 2, bc);
+            mma_step(xa[ks + 1], bn);
+        }
+    }
+
+    // epilogue.  acc[rb][cb][e]: row 32 RB wave + 32 rb + (e % 4) + 8 (e / 4) + 4 lh,
+    // column 32 cb + l32
+    if (splits > 1) {
+        // fp16 partials in accumulator layout [tile][split][wave][rb][cb][vp][lane]
+        // x 16 bytes: elements 8 vp .. 8 vp + 7 of acc[rb][cb] (rows of v = 2 vp,
+        // 2 vp + 1), summed in fp32 by gemm_reduce_kernel.  fp16 keeps the layer
+        // within its tolerance (rel-L2 2.9e-4 against 2.1e-4 for fp32 partials
+        // with fp16 output, at k = 14336) for half the bytes.
+        constexpr size_t kPerSplit = (size_t)kGemmWaves * RB * 4 * 2 * 64 * 8;  // halves
+        uint16_t *dst = partials + ((size_t)tile * splits + s) * kPerSplit + (size_t)wave * RB * 8 * 512 + lane * 8;
+        auto pk = [](float a, float b) {
+            return (uint32_t)float_to_half_bits(a) | ((uint32_t)float_to_half_bits(b) << 16);
+        };
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+                for (int vp = 0; vp < 2; ++vp) {
+                    const f16v &a = acc[rb][cb];
+                    const u4 d = {pk(a[8 * vp], a[8 * vp + 1]), pk(a[8 * vp + 2], a[8 * vp + 3]),
+                                  pk(a[8 * vp + 4], a[8 * vp + 5]), pk(a[8 * vp + 6], a[8 * vp + 7])};
+                    __builtin_nontemporal_store(d, (u4 *)(dst + ((rb * 4 + cb) * 2 + vp) * 512));
+                }
+        return;
+    }
+    const uint16_t *svp = (const uint16_t *)(colgroup + 2048 * K + 256);  // record (nb, 0)
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        float t[4][16];
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) t[cb][e] = acc[rb][cb][e];
+        gemm_rows_out<16>(t, lane, mt * BM + 32 * RB * wave + 32 * rb, svp, rows, y, y_f16, y_stride, (size_t)nb * 128,
+                          res, res_stride);
+    }
+}
+
+// Split-K reduction (split count > 1): one wave per (tile, row block blk =
+// RB wave + rb, vp) of the GEMM's partial layout; lane l sums its 4 x 16 bytes
+// (fp16) of every split in fp32 in split order (so the result does not depend on
+// the order the GEMM's workgroups ran in), then H128, 1/sqrt(128) and sv over its
+// 16 rows.
+template <int RB>
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(const uint16_t *__restrict__ partials, int splits, int nbs,
+                                                          const uint8_t *__restrict__ records, int bits, int kbs,
+                                                          void *y, int y_f16, size_t y_stride, int rows,
+                                                          int nwaves, const void *res, size_t res_stride) {
+    constexpr int BM = 32 * RB * kGemmWaves;
+    constexpr size_t kPerSplit = (size_t)kGemmWaves * RB * 4 * 2 * 64 * 8;  // halves
+    const int lane = threadIdx.x & 63;
+    const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (gw >= nwaves) return;
+    const int vp = gw & 1, blk = (gw >> 1) % (kGemmWaves * RB), tile = (gw >> 1) / (kGemmWaves * RB);
+    const int mt = tile / nbs, nb = tile - mt * nbs;
+    const uint16_t *src = partials + (size_t)tile * splits * kPerSplit + (size_t)blk * 8 * 512 + vp * 512 + lane * 8;
+    float t[4][8];
+#pragma unroll 1
+    for (int sp0 = 0; sp0 < splits; sp0 += 4) {  // loads of four splits in flight, then their sum in order
+        u4 in[4][4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int sp = sp0 + u < splits ? sp0 + u : splits - 1;
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) in[u][cb] = *(const u4 *)(src + (size_t)sp * kPerSplit + cb * 2 * 512);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (sp0 + u < splits)
+#pragma unroll
+                for (int cb = 0; cb < 4; ++cb) {
+                    const uint32_t w[4] = {in[u][cb].x, in[u][cb].y, in[u][cb].z, in[u][cb].w};
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) {
+                        const float v = half_bits_to_float((uint16_t)(w[q >> 1] >> (16 * (q & 1))));
+                        t[cb][q] = sp0 + u == 0 ? v : t[cb][q] + v;
+                    }
+                }
+    }
+    const uint16_t *svp = (const uint16_t *)(records + (size_t)nb * kbs * group_bytes(bits) + 2048 * bits + 256);
+    gemm_rows_out<8>(t, lane, mt * BM + 32 * blk + 16 * vp, svp, rows, y, y_f16, y_stride, (size_t)nb * 128, res,
+                     res_stride);
+}
+
+int gemm_tile_rows(size_t rows) { return rows <= 128 ? 128 : 256; }
+
+GemmPlan gemm_plan(size_t k, size_t n, size_t rows) {
+    GemmPlan p{};
+    p.nbs = (int)(n / 128);
+    p.kbs = (int)(k / 128);
+    p.bm = gemm_tile_rows(rows);
+    p.mtiles = (int)((rows + p.bm - 1) / p.bm);
+    const int tiles = p.nbs * p.mtiles;
+    // split k only below kGemmSplitTiles tiles; the split partials are summed by
+    // gemm_reduce_kernel
+    int s = tiles >= (int)kGemmSplitTiles ? 1 : (kGemmTargetWgs + tiles - 1) / tiles;
+    const int smax = p.kbs / 4 > 0 ? p.kbs / 4 : 1;
+    s = s < 1 ? 1 : (s > smax ? smax : s);
+    p.splits = s;
+    size_t off = 0;
+    p.counters_off = off;
+    off += counter_region_bytes(n);
+    p.xh_off = off;
+    off += ((size_t)p.mtiles * p.bm * k * 2 + 255) & ~(size_t)255;
+    p.partials_off = off;
+    if (s > 1) off += (size_t)tiles * s * p.bm * 128 * 2;  // fp16 partials
+    p.bytes = (off + 255) & ~(size_t)255;
+    return p;
+}
+
+template <int K, int CB>
+static void launch_gemm_kc(const uint8_t *rec, size_t k, uint16_t *xh, size_t rows, void *y, int y_f16,
+                           size_t y_stride, uint8_t *ws, const GemmPlan &p, hipStream_t stream, const void *res,
+                           size_t res_stride) {
+    const dim3 grid((unsigned)(p.mtiles * p.nbs * p.splits)), block(kGemmWaves * 64);
+    uint16_t *part = (uint16_t *)(ws + p.partials_off);
+    const int nwaves = p.mtiles * p.nbs * (p.bm / 16);  // reduction: one wave per 16 rows of a tile
+    const int kq = p.kbs / p.splits, kr = p.kbs % p.splits;
+    const dim3 rgrid((unsigned)((nwaves + 3) / 4));
+    if (p.bm == 128) {
+        gemm_kernel<K, CB, 1><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, kq, kr, xh, k, part,
+                                                          y, y_f16, y_stride, (int)rows, res, res_stride);
+        if (p.splits > 1)
+            gemm_reduce_kernel<1><<<rgrid, dim3(256), 0, stream>>>(part, p.splits, p.nbs, rec, K, p.kbs, y, y_f16,
+                                                                   y_stride, (int)rows, nwaves, res, res_stride);
+    } else {
+        gemm_kernel<K, CB, 2><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, kq, kr, xh, k, part,
+                                                          y, y_f16, y_stride, (int)rows, res, res_stride);
+        if (p.splits > 1)
+            gemm_reduce_kernel<2><<<rgrid, dim3(256), 0, stream>>>(part, p.splits, p.nbs, rec, K, p.kbs, y, y_f16,
+                                                                   y_stride, (int)rows, nwaves, res, res_stride);
+    }
+}
+
+template <int K>
+static hipError_t launch_gemm_k(const void *records, int cb, size_t k, const void *x, int x_f16, size_t rows,
+                                size_t x_stride, void *y, int y_f16, size_t y_stride, uint8_t *ws, const GemmPlan &p,
+                                hipStream_t stream, const void *res, size_t res_stride) {
+    const uint8_t *rec = (const uint8_t *)records;
+    uint16_t *xh = (uint16_t *)(ws + p.xh_off);
+    const int rows_padded = p.mtiles * p.bm;
+    gemm_xprep_kernel<<<dim3(p.kbs, rows_padded / 32), dim3(256), 0, stream>>>(rec, K, x, x_f16, x_stride, (int)rows,
+                                                                               p.kbs, xh);
+    switch (cb) {
+    case 0: launch_gemm_kc<K, 0>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream, res, res_stride); break;
+    case 1: launch_gemm_kc<K, 1>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream, res, res_stride); break;
+    default: launch_gemm_kc<K, 2>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream, res, res_stride); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm(const void *records, int bits, int cb, size_t k, size_t n, const void *x, int x_f16,
+                       size_t rows, size_t x_stride, void *y, int y_f16, size_t y_stride, void *workspace,
+                       const GemmPlan &p, hipStream_t stream, const void *res, size_t res_stride) {
+    (void)n;
+    uint8_t *ws = (uint8_t *)workspace;
+    switch (bits) {
+    case 1: return launch_gemm_k<1>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream, res,
+                                       res_stride);
+    case 2: return launch_gemm_k<2>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream, res,
+                                       res_stride);
+    case 3: return launch_gemm_k<3>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream, res,
+                                       res_stride);
+    case 4: return launch_gemm_k<4>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream, res,
+                                       res_stride);
+    case 5: return launch_gemm_k<5>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream, res,
+                                       res_stride);
+    case 6: return launch_gemm_k<6>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream, res,
+                                       res_stride);
+    case 7: return launch_gemm_k<7>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream, res,
+                                       res_stride);
+    default: return launch_gemm_k<8>(records, cb, k, x, x_f16, rows, x_stride, y, y_f16, y_stride, ws, p, stream, res,
+                                       res_stride);
+    }
+}
+
+}  // namespace exl3k

@@ -18,11 +18,18 @@ constexpr int kGemmWaves = 4;
 // Every plan starts with the GEMV's split-K arrival counters (one per column
 // group) and places nothing else there, so one workspace serves calls of any
 // row count (and any k) in turn: the counters return to zero at the end of
-// every GEMV call and no GEMM call touches them.  The GEMM splits k only while
-// it has fewer than kGemmSplitTiles output tiles; a second kernel sums its split
+// every GEMV call and no GEMM call touches them.  The region has at least
+// kCounterFloor slots whatever n is, so calls whose n differ but stay within
+// 128 * kCounterFloor = 65536 columns put every other region at the same offset
+// and never write over each other's counters.  The GEMM splits k only while it
+// has fewer than kGemmSplitTiles output tiles; a second kernel sums its split
 // partials.
 constexpr size_t kGemmSplitTiles = 512;
-inline size_t counter_region_bytes(size_t n) { return (n / 128 * 4 + 255) & ~(size_t)255; }
+constexpr size_t kCounterFloor = 512;
+inline size_t counter_region_bytes(size_t n) {
+    const size_t slots = n / 128 > kCounterFloor ? n / 128 : kCounterFloor;
+    return (slots * 4 + 255) & ~(size_t)255;
+}
 
 // Up to kGemvMaxTargets matrices that share k, the bit rate, the codebook and x,
 // served by one GEMV launch: column groups [nb_end[i-1], nb_end[i]) belong to
