@@ -344,7 +344,7 @@ def test_internal_workspace_under_capture(amd):
     assert err.value.status == amd.WORKSPACE_TOO_SMALL
     torch.cuda.synchronize()
     with torch.cuda.stream(s):
-        eager = amd.mul_mat(rd, bits, k, n, x, stream=s).clone()   # grows the internal workspace
+        eager = amd.mul_mat(rd, bits, k, n, x, out_dtype=torch.float16, stream=s).clone()  # grows the workspace
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):

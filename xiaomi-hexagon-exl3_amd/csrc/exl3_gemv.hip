@@ -60,7 +60,8 @@ constexpr size_t kGemvFragLds16 = 65536;  // the same for rows 9..16 (two workgr
 template <int K, int CB, int MODE>
 __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
     GemvTargets tg, int kbs, int splits, int kq, int kr, const void *__restrict__ x, int x_f16, size_t x_stride,
-    int rows, const uint8_t *__restrict__ dummy, float *__restrict__ partials, unsigned *__restrict__ counters,
+    int rows, const uint8_t *__restrict__ dummy, uint64_t *__restrict__ partials, unsigned *__restrict__ counters,
+    unsigned *__restrict__ gens,
     int y_f16, const uint8_t *__restrict__ xpre) {
     constexpr bool TWO = MODE >= 1, HILO = MODE <= 1;
     constexpr int W = kGemvWaves;
@@ -82,6 +83,8 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
     // grid (column group, split): no division on the way to the first loads.
     // Split s owns kq + (s < kr) records from kb0 (kq = kbs / splits, kr = kbs % splits)
     const int nb = blockIdx.x, s = blockIdx.y;
+    // generation tag of this call's split partials (read early: used at the exchange)
+    const unsigned gen = splits > 1 ? load_relaxed(gens + nb) : 0u;
     const int kb0 = s * kq + (s < kr ? s : kr), kb1 = kb0 + kq + (s < kr ? 1 : 0);
     const int nkb = kb1 - kb0;
     // the matrix of column group nb (targets share k, x and the bit rate)
@@ -404,40 +407,45 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
         }
     };
     if (splits > 1) {
-        float *mine = partials + ((size_t)nb * splits + s) * (size_t)nval;
+        uint64_t *mine = partials + ((size_t)nb * splits + s) * (size_t)nval;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int t = tid + i * NT;
-            if (t < nval) store_coherent(mine + t, psum[i]);
+            if (t < nval) store_tagged(mine + t, psum[i], gen);
         }
         if (!arrive_last(counters + nb, (unsigned)splits, &last_flag)) return;
         // the last workgroup: wave r sums row r's elements lane and lane + 64 over
         // the splits in split order (so the result does not depend on which
         // workgroup arrived last), all of a lane's loads in flight together,
         // straight into the registers of the output transform
-        const float *all = partials + (size_t)nb * splits * (size_t)nval;
+        const uint64_t *all = partials + (size_t)nb * splits * (size_t)nval;
         for (int rr = wave; rr < rows; rr += W) {
             constexpr int B = 16;
             float a0 = 0.f, a1 = 0.f;
             for (int base = 0; base < splits; base += B) {
-                float v0[B], v1[B];
+                uint64_t v0[B], v1[B];
 #pragma unroll
                 for (int jb = 0; jb < B; ++jb) {
                     const int sp = base + jb < splits ? base + jb : splits - 1;  // repeats are not added
-                    const float *q = all + (size_t)sp * nval + rr * 128 + lane;
-                    v0[jb] = load_coherent(q);
-                    v1[jb] = load_coherent(q + 64);
+                    const uint64_t *q = all + (size_t)sp * nval + rr * 128 + lane;
+                    v0[jb] = load_tagged(q);
+                    v1[jb] = load_tagged(q + 64);
                 }
 #pragma unroll
                 for (int jb = 0; jb < B; ++jb)
                     if (base + jb < splits) {
-                        a0 += v0[jb];
-                        a1 += v1[jb];
+                        const uint64_t *q = all + (size_t)(base + jb) * nval + rr * 128 + lane;
+                        a0 += tagged_value(q, v0[jb], gen);
+                        a1 += tagged_value(q + 64, v1[jb], gen);
                     }
             }
             finish_row(rr, a0, a1);
         }
-        if (tid == 0) reset_counter(counters + nb);  // self-reset for the next call
+        __syncthreads();  // every wave has read its partials: the next call may reuse them
+        if (tid == 0) {
+            store_relaxed(gens + nb, gen + 1);
+            store_relaxed(counters + nb, 0u);
+        }
         return;
     }
     // 6. (one workgroup per column group) output H128 per row from the LDS sums
@@ -524,11 +532,12 @@ GemvPlan gemv_plan(size_t k, size_t n, size_t rows) {
     p.nkw = (p.kbs + s - 1) / s;
     size_t off = 0;
     p.counters_off = off;
+    p.gens_off = off + counter_slots(n) * 4;
     off += counter_region_bytes(n);
     p.dummy_off = off;  // target of the stream's issues past a wave's last group (loaded, never used)
     off += kGemvDummyBytes;
     p.partials_off = off;
-    if (s > 1) off += (size_t)p.nbs * s * rows * 128 * 4;
+    if (s > 1) off += (size_t)p.nbs * s * rows * 128 * 8;  // generation-tagged fp32 partials
     off = (off + 255) & ~(size_t)255;
     p.xpre_off = off;  // rows > 16: prepared activations of up to kGemvMaxTargets matrices
     if (rows > 16) off += (size_t)kGemvMaxTargets * p.kbs * gemv_frag_bytes_per_kb(rows);
@@ -543,21 +552,21 @@ static hipError_t launch_gemv_kc(const GemvTargets &tg, const void *x, int x_f16
     // x fastest: workgroup (nb, s) is dispatched as nb + s nbs, as a 1-D grid would be
     const dim3 grid((unsigned)p.nbs, (unsigned)p.splits), block(kGemvWaves * 64);
     const int kq = p.kbs / p.splits, kr = p.kbs % p.splits;
-    float *part = (float *)(ws + p.partials_off);
-    unsigned *cnt = (unsigned *)(ws + p.counters_off);
+    uint64_t *part = (uint64_t *)(ws + p.partials_off);
+    unsigned *cnt = (unsigned *)(ws + p.counters_off), *gens = (unsigned *)(ws + p.gens_off);
     if (rows > 16) {
         uint16_t *xp = (uint16_t *)(ws + p.xpre_off);
         gemv_xprep_kernel<<<dim3((unsigned)((rows + 3) / 4), (unsigned)p.kbs, (unsigned)tg.count), dim3(256), 0,
                             stream>>>(tg, K, x, x_f16, x_stride, (int)rows, p.kbs, xp);
         gemv_kernel<K, CB, 2><<<grid, block, lds, stream>>>(tg, p.kbs, p.splits, kq, kr, x, x_f16, x_stride,
-                                                            (int)rows, ws + p.dummy_off, part, cnt, y_f16,
+                                                            (int)rows, ws + p.dummy_off, part, cnt, gens, y_f16,
                                                             (const uint8_t *)xp);
     } else if (rows > 8) {
         gemv_kernel<K, CB, 1><<<grid, block, lds, stream>>>(tg, p.kbs, p.splits, kq, kr, x, x_f16, x_stride,
-                                                            (int)rows, ws + p.dummy_off, part, cnt, y_f16, nullptr);
+                                                            (int)rows, ws + p.dummy_off, part, cnt, gens, y_f16, nullptr);
     } else {
         gemv_kernel<K, CB, 0><<<grid, block, lds, stream>>>(tg, p.kbs, p.splits, kq, kr, x, x_f16, x_stride,
-                                                            (int)rows, ws + p.dummy_off, part, cnt, y_f16, nullptr);
+                                                            (int)rows, ws + p.dummy_off, part, cnt, gens, y_f16, nullptr);
     }
     return hipGetLastError();
 }

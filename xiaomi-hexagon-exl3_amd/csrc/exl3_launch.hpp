@@ -15,21 +15,20 @@ constexpr int kGemvMaxRows = 32;
 constexpr int kGemvWaves = 8;     // waves per GEMV workgroup (a multiple of 4)
 constexpr int kGemmWaves = 4;
 
-// Every plan starts with the GEMV's split-K arrival counters (one per column
-// group) and places nothing else there, so one workspace serves calls of any
-// row count (and any k) in turn: the counters return to zero at the end of
-// every GEMV call and no GEMM call touches them.  The region has at least
-// kCounterFloor slots whatever n is, so calls whose n differ but stay within
-// 128 * kCounterFloor = 65536 columns put every other region at the same offset
-// and never write over each other's counters.  The GEMM splits k only while it
-// has fewer than kGemmSplitTiles output tiles; a second kernel sums its split
-// partials.
+// Every plan starts with the GEMV's split-K sync words and places nothing else
+// there: one arrival counter per column group, then one generation number per
+// column group (u32 each).  One workspace therefore serves calls of any row
+// count (and any k) in turn: the counters return to zero at the end of every
+// GEMV call, the generations only count up, and no GEMM call touches them.  The
+// region has at least kCounterFloor slots whatever n is, so calls whose n differ
+// but stay within 128 * kCounterFloor = 65536 columns put every other region at
+// the same offset and never write over each other's sync words.  The GEMM
+// splits k only while it has fewer than kGemmSplitTiles output tiles; a second
+// kernel sums its split partials.
 constexpr size_t kGemmSplitTiles = 512;
 constexpr size_t kCounterFloor = 512;
-inline size_t counter_region_bytes(size_t n) {
-    const size_t slots = n / 128 > kCounterFloor ? n / 128 : kCounterFloor;
-    return (slots * 4 + 255) & ~(size_t)255;
-}
+inline size_t counter_slots(size_t n) { return n / 128 > kCounterFloor ? n / 128 : kCounterFloor; }
+inline size_t counter_region_bytes(size_t n) { return (counter_slots(n) * 8 + 255) & ~(size_t)255; }
 
 // Up to kGemvMaxTargets matrices that share k, the bit rate, the codebook and x,
 // served by one GEMV launch: column groups [nb_end[i-1], nb_end[i]) belong to
@@ -57,7 +56,7 @@ struct DecodeBatch {
 
 struct GemvPlan {
     int nbs, kbs, splits, nkw;  // nkw: largest kb count of a split
-    size_t counters_off, dummy_off, partials_off, xpre_off, bytes;
+    size_t counters_off, gens_off, dummy_off, partials_off, xpre_off, bytes;
 };
 struct GemmPlan {
     int nbs, kbs, bm, mtiles, splits;  // bm: rows per workgroup tile (128 or 256)
