@@ -255,29 +255,6 @@ def graph_time(torch, stream, fn, per_graph, replays=3):
     return s_ev.elapsed_time(e_ev) / (replays * per_graph)
 
 
-def c2_matrices():
-    """The 151 weight matrices of the 2B hybrid model (k in, n out)."""
-    mats = []
-    for _ in range(24):
-        mats += [(2048, 6144), (2048, 6144), (6144, 2048)]      # gate, up, down
-    for _ in range(6):
-        mats += [(2048, 2048), (2048, 512), (2048, 512), (2048, 2048)]   # q, k, v, o
-    for _ in range(18):
-        mats += [(2048, 2048), (2048, 2048), (2048, 512)]       # linear-attention projections
-    mats.append((2048, 151936))                                  # vocabulary head
-    return mats
-
-
-def c2_bits(np, synth, mats):
-    """Bits per matrix from {2..6} by seed, redrawn until the weight-weighted mean is <= 5.0."""
-    w = np.array([k * n for k, n in mats], dtype=np.float64)
-    for attempt in range(1000):
-        b = (synth.splitmix64(2222 + attempt, len(mats)) % np.uint64(5)).astype(int) + 2
-        if float(np.sum(w * b) / np.sum(w)) <= 5.0:
-            return b
-    raise RuntimeError("no bit draw met the 5.0 bpw bound")
-
-
 def extra_configs(amd, torch, np, synth, stream, args):
     out = {}
     dev = torch.device("cuda", 0)
@@ -344,8 +321,8 @@ def extra_configs(amd, torch, np, synth, stream, args):
     del sets
 
     # C2: dequant-only sweep of the 151 matrices (upstream tile layout -> fp16), bit-exactness in tests
-    mats = c2_matrices()
-    bits_c2 = c2_bits(np, synth, mats)
+    mats = synth.c2_matrices()
+    bits_c2 = synth.c2_bits(mats)
     packed = [rand_u16(9000 + i, k2 * n2 * int(b2) // 16) for i, ((k2, n2), b2) in enumerate(zip(mats, bits_c2))]
     # every matrix decodes into its own region of one 2.9 GB output (as a model's
     # dequantized weight set would), so no write is absorbed by a cache

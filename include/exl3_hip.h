@@ -74,6 +74,46 @@ size_t exl3_hip_gemv_max_rows(void);
 int exl3_hip_supports_mul_mat(unsigned bits, unsigned codebook, size_t k, size_t n, size_t rows,
                               exl3_dtype xt, exl3_dtype yt);
 
+/* ---- engine-side op predicates (ggml supports_op) ------------------------
+ * The reference gates the ggml ops that touch an EXL3 tensor in its CPU
+ * backend's supports_op (patches/llama-exl3.patch:81-97).  A HIP backend asks
+ * exl3_hip_supports_op with the op's tensors described by plain values:
+ *   MUL_MAT    src0 EXL3 (types 43/44/45): ne0 and ne1 multiples of 128, ne2 = ne3 = 1,
+ *              src0 contiguous, src1 F32 or F16 (patch:81-84); here also dst F32
+ *              and the dimensions exl3_hip_mul_mat accepts
+ *   MUL_MAT_ID src0 EXL3: unsupported (patch:92-93)
+ *   GET_ROWS   src0 EXL3: ne0 and ne1 multiples of 128, ne2 = ne3 = 1, src1 I32
+ *              (patch:94-97); here also dst F32 or F16
+ *   CPY        dst or src0 EXL3: only a copy between contiguous tensors of the
+ *              same EXL3 type, i.e. a byte copy of group records (patch:71-72)
+ *   SET_ROWS   dst or src0 EXL3: unsupported (patch:69-72)
+ * Returns 1 (served), 0 (refused: keep the op off this backend) or -1 (no EXL3
+ * tensor in the op: not this library's decision). */
+typedef enum exl3_op {
+    EXL3_OP_MUL_MAT = 0,
+    EXL3_OP_MUL_MAT_ID = 1,
+    EXL3_OP_GET_ROWS = 2,
+    EXL3_OP_CPY = 3,
+    EXL3_OP_SET_ROWS = 4
+} exl3_op;
+
+/* ggml type ids used by the predicates (ggml.h enum ggml_type of the reference's
+ * llama.cpp revision; the EXL3 ids are include/exl3-block.h's 43/44/45) */
+#define EXL3_GGML_TYPE_F32 0u
+#define EXL3_GGML_TYPE_F16 1u
+#define EXL3_GGML_TYPE_I32 26u
+
+typedef struct exl3_tensor_info {
+    unsigned type;     /* ggml type id */
+    int64_t ne[4];     /* ggml ne[]: ne[0] is the row length */
+    int contiguous;    /* ggml_is_contiguous() */
+} exl3_tensor_info;
+
+/* dst and src0 are required; src1 is required for MUL_MAT, MUL_MAT_ID and GET_ROWS
+ * (NULL there: 0). */
+int exl3_hip_supports_op(exl3_op op, const exl3_tensor_info *dst, const exl3_tensor_info *src0,
+                         const exl3_tensor_info *src1);
+
 /* Device workspace bytes exl3_hip_mul_mat needs for (k, n) at any row count
  * 1..rows.  The workspace holds per-call staging and self-resetting completion
  * counters: zero-fill it once before its first use (exl3_hip_workspace_init).
@@ -250,6 +290,18 @@ exl3_status exl3_hip_model_matrix(const exl3_model *model, size_t index, char *n
                                   unsigned *bits, unsigned *codebook, size_t *k, size_t *n);
 /* device bytes of matrix index's group records (0 for a bad index) */
 size_t exl3_hip_model_record_bytes(const exl3_model *model, size_t index);
+/* Row-coded EXL3 embedding tables of the model: every <prefix>.trellis of rank 2
+ * (I16 [rows, groups * words]) that has a <prefix>.signs (F16 [groups, 256]),
+ * validated as the reference's model audit validates them
+ * (tools/inspect_model.py:78-90): words = 16 * bits + 1 per group, bits 1..8.
+ * Their decode is not implemented (the reference's runtime has none either).
+ * EXL3_OK with *count, or EXL3_INVAL_PARAMS with the audit's reason copied into
+ * error ("Invalid EXL3 embedding: <name>", "... groups: ...", "... bitrate: ..."). */
+exl3_status exl3_hip_model_embedding_tables(const exl3_model *model, size_t *count, char *error, size_t error_bytes);
+/* table index (name order): its prefix, rows, groups, bits and padded width
+ * (groups * 256) */
+exl3_status exl3_hip_model_embedding_table(const exl3_model *model, size_t index, char *name, size_t name_bytes,
+                                           size_t *rows, size_t *groups, unsigned *bits, size_t *width_padded);
 /* packs matrix index into group records at device pointer records (16-byte
  * aligned, exl3_hip_model_record_bytes long), ready for exl3_hip_mul_mat;
  * returns when they are complete.  k and n must be multiples of 128. */

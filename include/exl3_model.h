@@ -55,6 +55,16 @@ public:
      * pointer `records` (16-byte aligned, record_bytes() long) on `stream`;
      * returns after the records are complete.  k and n must be multiples of 128. */
     void upload_records(const Matrix & matrix, void * records, hipStream_t stream) const;
+    /* row-coded embedding tables (<prefix>.trellis [rows, groups * (16 bits + 1)] I16
+     * with <prefix>.signs [groups, 256] F16), validated as the reference's model
+     * audit does (tools/inspect_model.py:78-90); malformed tables throw
+     * std::runtime_error.  Listing only: their decode is not implemented. */
+    struct EmbeddingTable {
+        std::string prefix;
+        size_t rows, groups, width_padded;
+        unsigned bits;
+    };
+    std::vector<EmbeddingTable> embedding_tables() const;
 
 private:
     struct Impl;

@@ -75,3 +75,31 @@ def pack_records(packed, su, sv, bits):
 
 def group_bytes(bits):
     return 2048 * bits + 512
+
+
+def c2_matrices():
+    """The 151 weight matrices (k in, n out) of the synthetic 2B hybrid model of the
+    dequant sweep: 24 MLP blocks (gate, up 2048->6144, down 6144->2048), 6 full
+    attention blocks (q 2048->2048, k and v 2048->512, o 2048->2048), 18
+    linear-attention blocks (2048->2048, 2048->2048, 2048->512) and the vocabulary
+    head 2048->151936."""
+    mats = []
+    for _ in range(24):
+        mats += [(2048, 6144), (2048, 6144), (6144, 2048)]
+    for _ in range(6):
+        mats += [(2048, 2048), (2048, 512), (2048, 512), (2048, 2048)]
+    for _ in range(18):
+        mats += [(2048, 2048), (2048, 2048), (2048, 512)]
+    mats.append((2048, 151936))
+    return mats
+
+
+def c2_bits(mats):
+    """Bits per matrix from {2..6} by seed, redrawn until the weight-weighted mean
+    is <= 5.0 bits per weight."""
+    w = np.array([k * n for k, n in mats], dtype=np.float64)
+    for attempt in range(1000):
+        b = (splitmix64(2222 + attempt, len(mats)) % np.uint64(5)).astype(int) + 2
+        if float(np.sum(w * b) / np.sum(w)) <= 5.0:
+            return b
+    raise RuntimeError("no bit draw met the 5.0 bpw bound")

@@ -110,3 +110,44 @@ def test_oracle_exhaustive_vs_compiled_reference():
     r = subprocess.run([str(ROOT / "oracle" / "_ref" / "check_ref")], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "0 mismatches over 2^32" in r.stdout
+
+
+def test_ggml_op_predicates():
+    """exl3_hip_supports_op: the supports_op rules the reference applies to ops that
+    touch an EXL3 tensor (patches/llama-exl3.patch:69-97), one accepted and one
+    refused case per rule, and -1 for ops without an EXL3 tensor."""
+    import conftest
+    a = conftest.load_amd()
+    T = a.TensorInfo.of
+    F32, F16, I32, Q4, Q6, Q8 = a.GGML_F32, a.GGML_F16, a.GGML_I32, 43, 44, 45
+    k, n, rows = 2048, 6144, 7
+    w = T(Q4, [k, n])
+    # MUL_MAT (patch:81-84): 128-multiple 2-D contiguous weight, F32/F16 activations
+    assert a.supports_op(a.OP_MUL_MAT, T(F32, [n, rows]), w, T(F32, [k, rows])) == 1
+    assert a.supports_op(a.OP_MUL_MAT, T(F32, [n, rows]), T(Q8, [k, n]), T(F16, [k, rows])) == 1
+    assert a.supports_op(a.OP_MUL_MAT, T(F32, [n, 2, 3]), T(Q6, [k, n]), T(F16, [k, 2, 3])) == 1   # batched rows
+    assert a.supports_op(a.OP_MUL_MAT, T(F32, [n, rows]), w, T(30, [k, rows])) == 0               # BF16 input
+    assert a.supports_op(a.OP_MUL_MAT, T(F32, [n, rows]), T(Q4, [k + 64, n]), T(F32, [k + 64, rows])) == 0
+    assert a.supports_op(a.OP_MUL_MAT, T(F32, [n, rows]), T(Q4, [k, n - 16]), T(F32, [k, rows])) == 0
+    assert a.supports_op(a.OP_MUL_MAT, T(F32, [n, rows]), T(Q4, [k, n, 2]), T(F32, [k, rows])) == 0  # 3-D weight
+    assert a.supports_op(a.OP_MUL_MAT, T(F32, [n, rows]), T(Q4, [k, n], False), T(F32, [k, rows])) == 0
+    assert a.supports_op(a.OP_MUL_MAT, T(F16, [n, rows]), w, T(F32, [k, rows])) == 0              # dst not F32
+    assert a.supports_op(a.OP_MUL_MAT, T(F32, [n, rows]), w, None) == 0
+    assert a.supports_op(a.OP_MUL_MAT, T(F32, [n, rows]), T(F16, [k, n]), T(F32, [k, rows])) == -1
+    # MUL_MAT_ID (patch:92-93): never on EXL3 weights
+    assert a.supports_op(a.OP_MUL_MAT_ID, T(F32, [n, rows]), w, T(F32, [k, rows])) == 0
+    assert a.supports_op(a.OP_MUL_MAT_ID, T(F32, [n, rows]), T(F16, [k, n]), T(F32, [k, rows])) == -1
+    # GET_ROWS (patch:94-97): I32 ids into a 128-multiple 2-D table
+    assert a.supports_op(a.OP_GET_ROWS, T(F32, [k, 5]), w, T(I32, [5])) == 1
+    assert a.supports_op(a.OP_GET_ROWS, T(F16, [k, 5]), w, T(I32, [5])) == 1
+    assert a.supports_op(a.OP_GET_ROWS, T(F32, [k, 5]), w, T(27, [5])) == 0                       # I64 ids
+    assert a.supports_op(a.OP_GET_ROWS, T(F32, [k, 5]), T(Q4, [k, n, 1, 2]), T(I32, [5])) == 0
+    assert a.supports_op(a.OP_GET_ROWS, T(F32, [k, 5]), T(F16, [k, n]), T(I32, [5])) == -1
+    # CPY / SET_ROWS (patch:69-72): only a contiguous copy between tensors of one EXL3 type
+    assert a.supports_op(a.OP_CPY, T(Q4, [k, n]), w) == 1
+    assert a.supports_op(a.OP_CPY, T(Q6, [k, n]), w) == 0                  # type change
+    assert a.supports_op(a.OP_CPY, T(F16, [k, n]), w) == 0                 # dequantising copy
+    assert a.supports_op(a.OP_CPY, T(Q4, [k, n]), T(F32, [k, n])) == 0     # quantising copy
+    assert a.supports_op(a.OP_CPY, T(Q4, [k, n], False), w) == 0
+    assert a.supports_op(a.OP_SET_ROWS, T(Q4, [k, n]), T(F32, [k, 3]), T(I32, [3])) == 0
+    assert a.supports_op(a.OP_CPY, T(F16, [k, n]), T(F32, [k, n])) == -1

@@ -194,3 +194,73 @@ def test_cpp_model_api_program(tmp_path):
     r = subprocess.run([str(exe), str(tmp_path)], capture_output=True, text=True, timeout=300)
     print(r.stdout, r.stderr, flush=True)
     assert r.returncode == 0 and "PASS" in r.stdout
+
+
+def _with_embedding_table(header, data, manifest, rows, groups, bits, signs_cols=256, trellis_dtype="I16",
+                          signs_dtype="F16", words=None):
+    """adds a row-coded table emb.trellis [rows, groups * words] + emb.signs [groups, 256]
+    (tools/inspect_model.py:78-90) to a model and fixes the manifest's payload"""
+    words = 16 * bits + 1 if words is None else words
+    off = len(data)
+    width = {"I16": 2, "F16": 2, "F32": 4}
+    tb = rows * groups * words * width[trellis_dtype]
+    sb = groups * signs_cols * width[signs_dtype]
+    header = dict(header)
+    header["emb.trellis"] = {"dtype": trellis_dtype, "shape": [rows, groups * words], "data_offsets": [off, off + tb]}
+    header["emb.signs"] = {"dtype": signs_dtype, "shape": [groups, signs_cols], "data_offsets": [off + tb, off + tb + sb]}
+    manifest = dict(manifest)
+    manifest["weight_payload_bytes"] = off + tb + sb
+    manifest["reference_parameter_count"] = 10 ** 6     # keep the 5.0 bpw budget
+    return header, bytes(data) + bytes(tb + sb), manifest
+
+
+def test_row_coded_embedding_tables(tmp_path):
+    """Row-coded EXL3 embedding tables are listed with their geometry and
+    rejected, with the reference audit's messages, when malformed
+    (tools/inspect_model.py:78-90); the model itself still opens."""
+    amd = amd_lib()
+    cases = [  # (rows, groups, bits, kwargs, expected reason or None)
+        (6, 3, 4, {}, None),
+        (2, 1, 1, {}, None),
+        (4, 2, 8, {}, None),
+        (4, 2, 4, {"signs_cols": 128}, "Invalid EXL3 embedding: emb.trellis"),
+        (4, 2, 4, {"trellis_dtype": "F16"}, "Invalid EXL3 embedding: emb.trellis"),
+        (4, 2, 4, {"signs_dtype": "F32"}, "Invalid EXL3 embedding: emb.trellis"),
+        (4, 2, 4, {"words": 16 * 4}, "Invalid EXL3 embedding bitrate: emb.trellis"),    # no header word
+        (4, 2, 9, {}, "Invalid EXL3 embedding bitrate: emb.trellis"),                    # 9 bits
+        (4, 1, 0, {"words": 1}, "Invalid EXL3 embedding bitrate: emb.trellis"),          # 0 bits
+    ]
+    for i, (rows, groups, bits, kw, reason) in enumerate(cases):
+        d = tmp_path / f"m{i}"
+        d.mkdir()
+        write_model(d, *_with_embedding_table(*reference_case(), rows, groups, bits, **kw))
+        m, why = open_or_reason(d)
+        assert m is not None, (i, why)
+        with m:
+            if reason is None:
+                assert m.embedding_tables() == [("emb", rows, groups, bits, groups * 256)], i
+                assert m.matrices() == [("lm_head", 4, 2, 128, 128)]   # the table is not a matrix
+            else:
+                with pytest.raises(amd.Exl3Error) as e:
+                    m.embedding_tables()
+                assert reason in str(e.value), (i, str(e.value))
+    # group count that does not divide the code width
+    d = tmp_path / "groups"
+    d.mkdir()
+    header, data, manifest = _with_embedding_table(*reference_case(), 4, 3, 4)
+    header["emb.trellis"]["shape"] = [4, 3 * 65 + 1]
+    header["emb.trellis"]["data_offsets"][1] += 8
+    header["emb.signs"]["data_offsets"] = [o + 8 for o in header["emb.signs"]["data_offsets"]]
+    manifest["weight_payload_bytes"] += 8
+    write_model(d, header, bytes(data) + bytes(8), manifest)
+    with amd.Model(d) as m:
+        with pytest.raises(amd.Exl3Error) as e:
+            m.embedding_tables()
+        assert "Invalid EXL3 embedding groups: emb.trellis" in str(e.value)
+    with amd.Model(tmp_path / "m0") as m:   # the reference test's model has none
+        pass
+    d = tmp_path / "plain"
+    d.mkdir()
+    write_model(d, *reference_case())
+    with amd.Model(d) as m:
+        assert m.embedding_tables() == []

@@ -3,6 +3,7 @@
 // preconditions (src/exl3-ggml.cpp:56-57, src/exl3_codec.cpp:12-19,117-135,
 // patches/llama-exl3.patch:81-84,225-235) and turn them into status codes.
 #include "exl3_hip.h"
+#include "exl3-block.h"
 
 #include <hip/hip_runtime.h>
 
@@ -94,6 +95,46 @@ int exl3_hip_supports_mul_mat(unsigned bits, unsigned codebook, size_t k, size_t
                               exl3_dtype yt) {
     return valid_rate(bits, codebook) && valid_matrix(k, n, 128) && rows >= 1 && rows <= kMaxRows &&
            valid_dtype(xt) && valid_dtype(yt);
+}
+
+// patches/llama-exl3.patch:69-97: the supports_op rules for ops that touch an
+// EXL3 tensor, on plain tensor descriptions; plus the limits of this library's
+// kernels (exl3_hip_supports_mul_mat's dimensions, F32/F16 outputs).
+static bool is_exl3(const exl3_tensor_info *t) { return t && (t->type >= 43 && t->type <= 45); }
+static bool is_2d_groups(const exl3_tensor_info *t) {
+    return t->ne[0] > 0 && t->ne[1] > 0 && t->ne[0] % 128 == 0 && t->ne[1] % 128 == 0 && t->ne[2] == 1 &&
+           t->ne[3] == 1;
+}
+
+int exl3_hip_supports_op(exl3_op op, const exl3_tensor_info *dst, const exl3_tensor_info *src0,
+                         const exl3_tensor_info *src1) {
+    if (!dst || !src0) return 0;
+    switch (op) {
+    case EXL3_OP_CPY:
+    case EXL3_OP_SET_ROWS:
+        if (!is_exl3(dst) && !is_exl3(src0)) return -1;
+        return op == EXL3_OP_CPY && src0->type == dst->type && src0->contiguous && dst->contiguous;
+    case EXL3_OP_MUL_MAT_ID:
+        return is_exl3(src0) ? 0 : -1;
+    case EXL3_OP_MUL_MAT: {
+        if (!is_exl3(src0)) return -1;
+        if (!src1 || !is_2d_groups(src0) || !src0->contiguous) return 0;
+        if (src1->type != EXL3_GGML_TYPE_F32 && src1->type != EXL3_GGML_TYPE_F16) return 0;
+        if (dst->type != EXL3_GGML_TYPE_F32) return 0;
+        const int64_t rows = src1->ne[1] * src1->ne[2] * src1->ne[3];
+        if (src1->ne[0] != src0->ne[0] || rows < 1) return 0;
+        return exl3_hip_supports_mul_mat(exl3_type_bits(src0->type), EXL3_CB_MUL1, (size_t)src0->ne[0],
+                                         (size_t)src0->ne[1], (size_t)rows,
+                                         src1->type == EXL3_GGML_TYPE_F16 ? EXL3_F16 : EXL3_F32, EXL3_F32);
+    }
+    case EXL3_OP_GET_ROWS:
+        if (!is_exl3(src0)) return -1;
+        if (!src1 || !is_2d_groups(src0) || src1->type != EXL3_GGML_TYPE_I32) return 0;
+        if (dst->type != EXL3_GGML_TYPE_F32 && dst->type != EXL3_GGML_TYPE_F16) return 0;
+        return exl3_hip_supports_mul_mat(exl3_type_bits(src0->type), EXL3_CB_MUL1, (size_t)src0->ne[0],
+                                         (size_t)src0->ne[1], 1, EXL3_F32, EXL3_F32);
+    }
+    return 0;
 }
 
 // The largest plan over every row count 1..rows, so one workspace serves all

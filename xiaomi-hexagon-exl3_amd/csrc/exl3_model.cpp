@@ -173,6 +173,13 @@ std::vector<Model::Matrix> Model::matrices() const {
     return out;
 }
 
+std::vector<Model::EmbeddingTable> Model::embedding_tables() const {
+    std::vector<EmbeddingTable> out;
+    for (const exl3fmt::EmbeddingTableEntry &e : exl3fmt::list_embedding_tables(impl->om.index))
+        out.push_back({e.prefix, e.rows, e.groups, e.width_padded, e.bits});
+    return out;
+}
+
 size_t Model::record_bytes(const Matrix &m) const { return (m.n / 128) * (m.k / 128) * (2048 * (size_t)m.bits + 512); }
 
 void Model::upload_records(const Matrix &m, void *records, hipStream_t stream) const {
@@ -279,6 +286,35 @@ exl3_status exl3_hip_model_upload_records(const exl3_model *m, size_t index, voi
         return EXL3_INVAL_PARAMS;
     } catch (...) {
         return EXL3_HIP_ERROR;
+    }
+}
+
+exl3_status exl3_hip_model_embedding_tables(const exl3_model *m, size_t *count, char *error, size_t error_bytes) {
+    if (!m || !count) return EXL3_INVAL_PARAMS;
+    try {
+        *count = m->model.embedding_tables().size();
+        return EXL3_OK;
+    } catch (const std::exception &e) {
+        set_error(error, error_bytes, e.what());
+        return EXL3_INVAL_PARAMS;
+    }
+}
+
+exl3_status exl3_hip_model_embedding_table(const exl3_model *m, size_t index, char *name, size_t name_bytes,
+                                           size_t *rows, size_t *groups, unsigned *bits, size_t *width_padded) {
+    if (!m) return EXL3_INVAL_PARAMS;
+    try {
+        const std::vector<exl3::Model::EmbeddingTable> tables = m->model.embedding_tables();
+        if (index >= tables.size()) return EXL3_INVAL_PARAMS;
+        const exl3::Model::EmbeddingTable &t = tables[index];
+        set_error(name, name_bytes, t.prefix.c_str());
+        if (rows) *rows = t.rows;
+        if (groups) *groups = t.groups;
+        if (bits) *bits = t.bits;
+        if (width_padded) *width_padded = t.width_padded;
+        return EXL3_OK;
+    } catch (const std::exception &) {
+        return EXL3_INVAL_PARAMS;
     }
 }
 

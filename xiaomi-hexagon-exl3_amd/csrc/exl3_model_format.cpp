@@ -260,6 +260,35 @@ std::vector<MatrixEntry> list_matrices(const TensorIndex &index, const uint8_t *
     return out;
 }
 
+std::vector<EmbeddingTableEntry> list_embedding_tables(const TensorIndex &index) {
+    static const std::string kTrellis = ".trellis";
+    std::vector<EmbeddingTableEntry> out;
+    for (const TensorEntry &t : index.entries) {
+        if (!ends_with(t.name, kTrellis)) continue;
+        const std::string prefix = t.name.substr(0, t.name.size() - kTrellis.size());
+        const TensorEntry *signs = index.find(prefix + ".signs");
+        if (!signs) continue;  // a matrix trellis
+        // [rows, groups * words] I16 codes with [groups, 256] F16 signs
+        const bool shape_ok = t.dims.size() == 2 && t.dtype == DType::I16 && signs->dtype == DType::F16 &&
+                              signs->dims.size() == 2 && signs->dims[1] == 256;
+        if (!shape_ok) reject("Invalid EXL3 embedding: " + t.name);
+        const size_t groups = signs->dims[0];
+        if (groups == 0 || t.dims[1] % groups) reject("Invalid EXL3 embedding groups: " + t.name);
+        // each group of a row: one 16-bit header word plus 16 words per bit of rate
+        const size_t words = t.dims[1] / groups;
+        if ((words - 1) % 16 || (words - 1) / 16 < 1 || (words - 1) / 16 > 8)
+            reject("Invalid EXL3 embedding bitrate: " + t.name);
+        EmbeddingTableEntry e;
+        e.prefix = prefix;
+        e.rows = t.dims[0];
+        e.groups = groups;
+        e.width_padded = groups * 256;
+        e.bits = unsigned((words - 1) / 16);
+        out.push_back(std::move(e));
+    }
+    return out;
+}
+
 OpenedModel open_model(const std::string &directory) {
     OpenedModel om;
     om.file = WeightFile::map(directory + "/model.safetensors");

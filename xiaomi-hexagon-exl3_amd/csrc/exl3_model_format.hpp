@@ -96,6 +96,16 @@ struct MatrixEntry {
 };
 std::vector<MatrixEntry> list_matrices(const TensorIndex &index, const uint8_t *file);
 
+// Row-coded EXL3 embedding tables: every <prefix>.trellis of rank 2 with a
+// <prefix>.signs, checked as the reference's model audit checks them
+// (tools/inspect_model.py:78-90); throws std::runtime_error with its messages.
+struct EmbeddingTableEntry {
+    std::string prefix;
+    size_t rows = 0, groups = 0, width_padded = 0;
+    unsigned bits = 0;
+};
+std::vector<EmbeddingTableEntry> list_embedding_tables(const TensorIndex &index);
+
 // The whole directory through passes 1-4 (what exl3::Model's constructor does
 // before any device work).
 struct OpenedModel {

@@ -25,7 +25,22 @@ EXPORTS = [
     "exl3_hip_model_hidden_size", "exl3_hip_model_vocab_size", "exl3_hip_model_bits_per_weight",
     "exl3_hip_model_embedding", "exl3_hip_model_matrix_count", "exl3_hip_model_matrix", "exl3_hip_model_record_bytes",
     "exl3_hip_model_upload_records", "exl3_hip_iface_matmul_workspace_bytes", "exl3_hip_iface_matmul",
+    "exl3_hip_supports_op", "exl3_hip_model_embedding_tables", "exl3_hip_model_embedding_table",
 ]
+
+# ggml op predicates (exl3_hip_supports_op)
+OP_MUL_MAT, OP_MUL_MAT_ID, OP_GET_ROWS, OP_CPY, OP_SET_ROWS = range(5)
+GGML_F32, GGML_F16, GGML_I32 = 0, 1, 26
+
+
+class TensorInfo(ctypes.Structure):
+    """exl3_tensor_info: a ggml tensor's type, ne[4] and contiguity"""
+    _fields_ = [("type", ctypes.c_uint), ("ne", ctypes.c_int64 * 4), ("contiguous", ctypes.c_int)]
+
+    @classmethod
+    def of(cls, type_, ne, contiguous=True):
+        ne = list(ne) + [1] * (4 - len(ne))
+        return cls(type_, (ctypes.c_int64 * 4)(*ne), int(contiguous))
 
 
 class Exl3Error(RuntimeError):
@@ -95,6 +110,14 @@ def load(path=LIB_PATH):
     L.exl3_hip_iface_matmul_workspace_bytes.argtypes = [u, sz, sz, sz]
     L.exl3_hip_iface_matmul.restype = i
     L.exl3_hip_iface_matmul.argtypes = [u, u, sz, sz, sz, vp, vp, vp, vp, vp, vp, sz, st]
+    ti = ctypes.POINTER(TensorInfo)
+    L.exl3_hip_supports_op.restype = i
+    L.exl3_hip_supports_op.argtypes = [i, ti, ti, ti]
+    L.exl3_hip_model_embedding_tables.restype = i
+    L.exl3_hip_model_embedding_tables.argtypes = [vp, ctypes.POINTER(sz), ctypes.c_char_p, sz]
+    L.exl3_hip_model_embedding_table.restype = i
+    L.exl3_hip_model_embedding_table.argtypes = [vp, sz, ctypes.c_char_p, sz, ctypes.POINTER(sz), ctypes.POINTER(sz),
+                                                 ctypes.POINTER(u), ctypes.POINTER(sz)]
     return L
 
 
@@ -303,6 +326,25 @@ class Model:
             out.append((name.value.decode(), b.value, c.value, kk.value, nn.value))
         return out
 
+    def embedding_tables(self):
+        """[(prefix, rows, groups, bits, width_padded)] of the row-coded embedding
+        tables; raises Exl3Error with the audit's reason for a malformed one"""
+        count = ctypes.c_size_t()
+        err = ctypes.create_string_buffer(512)
+        st = lib().exl3_hip_model_embedding_tables(self._h, ctypes.byref(count), err, len(err))
+        if st != OK:
+            raise Exl3Error(st, "model_embedding_tables: " + err.value.decode(errors="replace"))
+        out = []
+        for idx in range(count.value):
+            name = ctypes.create_string_buffer(1024)
+            rows, groups, width = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
+            bits = ctypes.c_uint()
+            _check(lib().exl3_hip_model_embedding_table(self._h, idx, name, len(name), ctypes.byref(rows),
+                                                        ctypes.byref(groups), ctypes.byref(bits), ctypes.byref(width)),
+                   "model_embedding_table")
+            out.append((name.value.decode(), rows.value, groups.value, bits.value, width.value))
+        return out
+
     def upload_records(self, index, device="cuda", stream=None):
         """uint8 CUDA tensor of matrix index's group records (for mul_mat)"""
         import torch
@@ -310,6 +352,12 @@ class Model:
         rec = torch.empty(nbytes, dtype=torch.uint8, device=device)
         _check(lib().exl3_hip_model_upload_records(self._h, index, _ptr(rec), _stream(stream)), "model_upload_records")
         return rec
+
+
+def supports_op(op, dst, src0, src1=None):
+    """exl3_hip_supports_op: 1 served, 0 refused, -1 no EXL3 tensor involved"""
+    return lib().exl3_hip_supports_op(op, ctypes.byref(dst), ctypes.byref(src0),
+                                      ctypes.byref(src1) if src1 is not None else None)
 
 
 def codebook_values(states, codebook, out=None, stream=None):
