@@ -147,6 +147,20 @@ exl3_status exl3_hip_mul_mat(const void *records, unsigned bits, unsigned codebo
                              void *y, exl3_dtype yt, size_t y_row_stride,
                              void *workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* exl3_hip_mul_mat without a workspace and without any allocation: no
+ * counterpart in the reference; for callers that cannot allocate (code under
+ * HIP-graph capture, serving loops or harnesses that forbid hipMalloc).  The
+ * workspace is a 64 MiB device array inside the library, one per GPU, held
+ * until the process ends; a call whose exl3_hip_mul_mat_workspace_bytes(k, n,
+ * rows) exceeds it returns EXL3_WORKSPACE_TOO_SMALL, and n above 65536 returns
+ * EXL3_INVAL_PARAMS, before anything is enqueued.  Every call on a GPU shares
+ * that GPU's array: calls that overlap on one GPU (different streams, or
+ * threads without ordering) race and give wrong results; order them on one
+ * stream.  Results equal exl3_hip_mul_mat's bit for bit. */
+exl3_status exl3_hip_mul_mat_noalloc(const void *records, unsigned bits, unsigned codebook, size_t k, size_t n,
+                                     const void *x, exl3_dtype xt, size_t rows, size_t x_row_stride,
+                                     void *y, exl3_dtype yt, size_t y_row_stride, hipStream_t stream);
+
 /* y = residual + layer(x): the graph ADD(MUL_MAT(w, x), residual) of
  * tests/test-exl3-graph.cpp:53-55 in one call, the sum formed in fp32 and
  * rounded once to yt.  residual: device, rows x n of yt, row stride

@@ -26,6 +26,7 @@ EXPORTS = [
     "exl3_hip_model_embedding", "exl3_hip_model_matrix_count", "exl3_hip_model_matrix", "exl3_hip_model_record_bytes",
     "exl3_hip_model_upload_records", "exl3_hip_iface_matmul_workspace_bytes", "exl3_hip_iface_matmul",
     "exl3_hip_supports_op", "exl3_hip_model_embedding_tables", "exl3_hip_model_embedding_table",
+    "exl3_hip_mul_mat_noalloc",
 ]
 
 # ggml op predicates (exl3_hip_supports_op)
@@ -68,6 +69,8 @@ def load(path=LIB_PATH):
     L.exl3_hip_workspace_init.argtypes = [vp, sz, st]
     L.exl3_hip_mul_mat.restype = i
     L.exl3_hip_mul_mat.argtypes = [vp, u, u, sz, sz, vp, i, sz, sz, vp, i, sz, vp, sz, st]
+    L.exl3_hip_mul_mat_noalloc.restype = i
+    L.exl3_hip_mul_mat_noalloc.argtypes = [vp, u, u, sz, sz, vp, i, sz, sz, vp, i, sz, st]
     L.exl3_hip_mul_mat_add.restype = i
     L.exl3_hip_decode_batch.restype = i
     L.exl3_hip_decode_batch.argtypes = [vp, sz, i, u, st]
