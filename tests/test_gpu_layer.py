@@ -286,9 +286,9 @@ def test_concurrent_streams(amd):
 def test_one_workspace_serves_mixed_widths(amd):
     """One caller workspace shared by layers of different n (all <= 65536) and
     both kernels: a GEMM call at n=2048 (its activation staging sits behind the
-    counter region), then GEMV calls at n=14336 (more column groups, so more
-    counters) and a gate/up group (n = 2 x 6144).  The counter region does not
-    depend on n, so no call writes over another's counters: every result equals
+    sync words and the split-K exchange), then GEMV calls at n=14336 (more column
+    groups, so more sync words) and a gate/up group (n = 2 x 6144).  Those regions
+    do not depend on n, so no call writes over another's: every result equals
     the one from a fresh workspace, over two rounds of the sequence."""
     import torch
     cases = {  # name: (k, [n...], rows, bits)
@@ -354,3 +354,56 @@ def test_internal_workspace_under_capture(amd):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(y, eager)
+
+
+# bytes every workspace of n <= 65536 starts with: 512 64-bit arrival counters,
+# then the 16 MiB of split-K hand-off words (both zero between calls)
+SHARED_PREFIX = 512 * 8 + (16 << 20)
+
+
+def test_exchange_left_empty(amd):
+    """The split-K hand-off leaves the workspace's sync words and exchange zero
+    after every GEMV call (its last workgroups empty what they read), and GEMM
+    calls never write there: a caller workspace used for GEMV calls of 1..32
+    rows, a group call and GEMM calls is zero over its first SHARED_PREFIX bytes
+    after each call, and every result equals the one from a fresh workspace."""
+    import torch
+    k, n, bits = 14336, 4096, 4
+    rd = dev(make_layer(303, k, n, bits))
+    seq = [1, 8, 16, 32, 64, 2, 17, 512, 9, 1]
+    ws = amd.new_workspace(k, n, max(seq))
+    assert ws.numel() >= SHARED_PREFIX
+    for i, rows in enumerate(seq):
+        x = torch.from_numpy(synth.activations(1300 + rows, rows, k)).cuda()
+        y = amd.mul_mat(rd, bits, k, n, x, workspace=ws).clone()
+        fresh = amd.mul_mat(rd, bits, k, n, x, workspace=amd.new_workspace(k, n, rows))
+        torch.cuda.synchronize()
+        assert torch.equal(y, fresh), f"call {i} rows={rows}"
+        nz = int(torch.count_nonzero(ws[:SHARED_PREFIX]))
+        assert nz == 0, f"call {i} rows={rows}: {nz} nonzero bytes left in the sync words / exchange"
+    mats = [(dev(make_layer(1400 + j, 2048, 6144, 4)), 6144) for j in range(2)]
+    wsg = amd.new_workspace(2048, 2 * 6144, 8)
+    for rows in (3, 8):
+        x = torch.from_numpy(synth.activations(1410 + rows, rows, 2048)).cuda()
+        amd.mul_mat_group(mats, 4, 2048, x, workspace=wsg)
+        torch.cuda.synchronize()
+        assert int(torch.count_nonzero(wsg[:SHARED_PREFIX])) == 0, f"group rows={rows}"
+
+
+def test_gemv_partials_beyond_exchange_run_as_gemm(amd):
+    """k=16384, n=8320 at 32 rows: the GEMV's split partials (1040 column-group
+    splits x 32 rows x 512 B = 17 MB) would not fit the 16 MiB exchange, so the
+    call runs as a GEMM; at 16 rows they fit and the GEMV runs.  The 32-row
+    result matches the two 16-row GEMV halves within the layer tolerance, and the
+    workspace's exchange stays zero."""
+    import torch
+    k, n, bits = 16384, 8320, 2
+    rd = dev(make_layer(1500, k, n, bits))
+    x = torch.from_numpy(synth.activations(1501, 32, k)).cuda()
+    ws = amd.new_workspace(k, n, 32)
+    y32 = amd.mul_mat(rd, bits, k, n, x, workspace=ws)
+    halves = torch.cat([amd.mul_mat(rd, bits, k, n, x[:16].contiguous(), workspace=ws),
+                        amd.mul_mat(rd, bits, k, n, x[16:].contiguous(), workspace=ws)])
+    torch.cuda.synchronize()
+    assert_layer_close(y32.cpu().numpy(), halves.cpu().numpy().astype(np.float64), what="GEMM fallback vs GEMV")
+    assert int(torch.count_nonzero(ws[:SHARED_PREFIX])) == 0

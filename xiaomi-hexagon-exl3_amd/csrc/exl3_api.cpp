@@ -143,7 +143,10 @@ size_t exl3_hip_mul_mat_workspace_bytes(size_t k, size_t n, size_t rows) {
     if (!valid_matrix(k, n, 128) || rows < 1 || rows > kMaxRows) return 0;
     size_t need = 0;
     const size_t gemv_rows = rows < (size_t)exl3k::kGemvMaxRows ? rows : (size_t)exl3k::kGemvMaxRows;
-    for (size_t r = 1; r <= gemv_rows; ++r) need = std::max(need, exl3k::gemv_plan(k, n, r).bytes);
+    for (size_t r = 1; r <= gemv_rows; ++r) {
+        const exl3k::GemvPlan p = exl3k::gemv_plan(k, n, r);
+        need = std::max(need, p.fits ? p.bytes : exl3k::gemm_plan(k, n, r).bytes);
+    }
     // GEMM plans: one tile height per row range, the largest row count of each
     // m-tile count within it
     for (size_t r = exl3k::kGemvMaxRows + 1; r <= rows;) {
@@ -169,7 +172,7 @@ static exl3_status mul_mat_impl(const void *records, unsigned bits, unsigned cod
     if (!records || !x || !y || !aligned(records, 16)) return EXL3_INVAL_PARAMS;
     if (!aligned(x, dtype_size(xt)) || !aligned(y, dtype_size(yt))) return EXL3_INVAL_PARAMS;
     if (x_row_stride < k || y_row_stride < n) return EXL3_INVAL_PARAMS;
-    const bool gemv = rows <= (size_t)exl3k::kGemvMaxRows;
+    const bool gemv = exl3k::gemv_serves(k, n, rows);
     const size_t need = exl3_hip_mul_mat_workspace_bytes(k, n, rows);
     if (workspace) {
         if (!aligned(workspace, 256)) return EXL3_INVAL_PARAMS;
@@ -226,7 +229,7 @@ exl3_status exl3_hip_mul_mat_group(const exl3_matrix_desc *mats, size_t count, u
         n_total += m.n;
     }
     if (!x || !aligned(x, dtype_size(xt)) || x_row_stride < k || n_total > kMaxDim) return EXL3_INVAL_PARAMS;
-    if (rows > (size_t)exl3k::kGemvMaxRows) {  // GEMM row counts: one call per matrix, each a full-size launch
+    if (!exl3k::gemv_serves(k, n_total, rows)) {  // GEMM: one call per matrix, each a full-size launch
         for (size_t i = 0; i < count; ++i) {
             const exl3_status st = exl3_hip_mul_mat(mats[i].records, bits, codebook, k, mats[i].n, x, xt, rows,
                                                     x_row_stride, mats[i].y, yt, mats[i].y_row_stride, workspace,

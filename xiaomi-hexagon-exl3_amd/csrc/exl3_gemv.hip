@@ -57,11 +57,13 @@ constexpr size_t kGemvFragLds16 = 65536;  // the same for rows 9..16 (two workgr
 // MODE 2 (rows 17..32): two blocks of 16 rows each, fp16 activations without the
 // lo halves, prepared once per call by gemv_xprep_kernel (xpre) and copied into
 // LDS instead of being transformed again by every column group.
+// amdgpu_waves_per_eu(4): two workgroups per CU.  Without it the compiler places
+// the VGPR that holds spilled SGPRs (rows 17..32) at v222, and the kernel then
+// runs one workgroup per CU.
 template <int K, int CB, int MODE>
-__global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
+__global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void gemv_kernel(
     GemvTargets tg, int kbs, int splits, int kq, int kr, const void *__restrict__ x, int x_f16, size_t x_stride,
-    int rows, const uint8_t *__restrict__ dummy, uint64_t *__restrict__ partials, unsigned *__restrict__ counters,
-    unsigned *__restrict__ gens,
+    int rows, const uint8_t *__restrict__ dummy, uint32_t *__restrict__ partials, uint64_t *__restrict__ sync,
     int y_f16, const uint8_t *__restrict__ xpre) {
     constexpr bool TWO = MODE >= 1, HILO = MODE <= 1;
     constexpr int W = kGemvWaves;
@@ -72,7 +74,7 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
     // K <= 2 keeps them within 128 VGPRs (two workgroups per CU)
     constexpr int D = TWO && K <= 2 ? 8 : GemvStream<K>::DEPTH;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    __shared__ int last_flag;
+    __shared__ unsigned claim_lds;  // arrivals before this workgroup's (split-K)
     uint8_t *frag = smem;
     // B fragments of one (kb, r4, half): [kg][hl][row] x 16 bytes (MODE 2: [kg][row])
     const int blk_bytes = (HILO ? 128 : 64) * rows;
@@ -83,8 +85,6 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
     // grid (column group, split): no division on the way to the first loads.
     // Split s owns kq + (s < kr) records from kb0 (kq = kbs / splits, kr = kbs % splits)
     const int nb = blockIdx.x, s = blockIdx.y;
-    // generation tag of this call's split partials (read early: used at the exchange)
-    const unsigned gen = splits > 1 ? load_relaxed(gens + nb) : 0u;
     const int kb0 = s * kq + (s < kr ? s : kr), kb1 = kb0 + kq + (s < kr ? 1 : 0);
     const int nkb = kb1 - kb0;
     // the matrix of column group nb (targets share k, x and the bit rate)
@@ -369,6 +369,7 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
         }
     }
     __syncthreads();
+    // the workgroup's partial: element t = row * 128 + column, the P wave partials summed
     constexpr int PER = ((MODE == 2 ? 32 : MODE == 1 ? 16 : 8) * 128 + NT - 1) / NT;
     float psum[PER];
 #pragma unroll
@@ -407,45 +408,69 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(
         }
     };
     if (splits > 1) {
-        uint64_t *mine = partials + ((size_t)nb * splits + s) * (size_t)nval;
+        // every workgroup hands its partial over in the exchange, waits for those
+        // stores to complete (so the last workgroup finds them in place and its
+        // re-read below stays a formality) and claims its arrival
+        uint32_t *mine = partials + ((size_t)nb * splits + s) * (size_t)nval;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int t = tid + i * NT;
-            if (t < nval) store_tagged(mine + t, psum[i], gen);
+            if (t < nval) store_exchange(mine + t, psum[i]);
         }
-        if (!arrive_last(counters + nb, (unsigned)splits, &last_flag)) return;
+        wait_stores();
+        __syncthreads();
+        if (tid == 0) claim_lds = claim_arrival(sync + nb);
+        __syncthreads();
+        if (claim_lds != (unsigned)splits - 1) return;
         // the last workgroup: wave r sums row r's elements lane and lane + 64 over
         // the splits in split order (so the result does not depend on which
-        // workgroup arrived last), all of a lane's loads in flight together,
-        // straight into the registers of the output transform
-        const uint64_t *all = partials + (size_t)nb * splits * (size_t)nval;
+        // workgroup arrived last), a batch of splits' loads in flight together,
+        // straight into the registers of the output transform.  A word still
+        // empty is read again (with the rest of its batch) until it is full.
+        uint32_t *all = partials + (size_t)nb * splits * (size_t)nval;
         for (int rr = wave; rr < rows; rr += W) {
             constexpr int B = 16;
             float a0 = 0.f, a1 = 0.f;
             for (int base = 0; base < splits; base += B) {
-                uint64_t v0[B], v1[B];
+                uint32_t v0[B], v1[B];
+                auto load_batch = [&](int bs, int rw) {
 #pragma unroll
-                for (int jb = 0; jb < B; ++jb) {
-                    const int sp = base + jb < splits ? base + jb : splits - 1;  // repeats are not added
-                    const uint64_t *q = all + (size_t)sp * nval + rr * 128 + lane;
-                    v0[jb] = load_tagged(q);
-                    v1[jb] = load_tagged(q + 64);
+                    for (int jb = 0; jb < B; ++jb) {
+                        const int sp = bs + jb < splits ? bs + jb : splits - 1;  // repeats are not used
+                        const uint32_t *q = all + (size_t)sp * nval + rw * 128 + lane;
+                        v0[jb] = load_exchange(q);
+                        v1[jb] = load_exchange(q + 64);
+                    }
+                };
+                load_batch(base, rr);
+                auto any_empty = [&]() {
+                    int z = 0;
+#pragma unroll
+                    for (int jb = 0; jb < B; ++jb)
+                        if (base + jb < splits) z |= (v0[jb] == 0u) | (v1[jb] == 0u);
+                    return z != 0;
+                };
+                for (int pass = 0; __builtin_amdgcn_ballot_w64(any_empty()) && pass < kExchangeSpinLimit; ++pass) {
+                    __builtin_amdgcn_s_sleep(2);
+                    // the addresses are formed again in every pass (the empty asm hides
+                    // that they repeat), so they hold no registers across the loop
+                    int bs = base, rw = rr;
+                    asm volatile("" : "+s"(bs), "+s"(rw));
+                    load_batch(bs, rw);  // a full word keeps its value until the clearing below
                 }
 #pragma unroll
                 for (int jb = 0; jb < B; ++jb)
-                    if (base + jb < splits) {
-                        const uint64_t *q = all + (size_t)(base + jb) * nval + rr * 128 + lane;
-                        a0 += tagged_value(q, v0[jb], gen);
-                        a1 += tagged_value(q + 64, v1[jb], gen);
+                    if (base + jb < splits) {  // a word that never filled: a loud result, not a hang
+                        a0 += v0[jb] ? exchange_value(v0[jb]) : __builtin_nanf("");
+                        a1 += v1[jb] ? exchange_value(v1[jb]) : __builtin_nanf("");
                     }
             }
             finish_row(rr, a0, a1);
         }
-        __syncthreads();  // every wave has read its partials: the next call may reuse them
-        if (tid == 0) {
-            store_relaxed(gens + nb, gen + 1);
-            store_relaxed(counters + nb, 0u);
-        }
+        // every word has been read: empty them and the arrival count for the next call
+        __syncthreads();
+        for (int t = tid; t < splits * nval; t += NT) clear_exchange(all + t);
+        if (tid == 0) clear_sync(sync + nb);
         return;
     }
     // 6. (one workgroup per column group) output H128 per row from the LDS sums
@@ -530,19 +555,21 @@ GemvPlan gemv_plan(size_t k, size_t n, size_t rows) {
     }
     p.splits = s;
     p.nkw = (p.kbs + s - 1) / s;
-    size_t off = 0;
-    p.counters_off = off;
-    p.gens_off = off + counter_slots(n) * 4;
-    off += counter_region_bytes(n);
+    p.counters_off = 0;
+    p.partials_off = exchange_offset(n);
+    p.exchange_bytes = s > 1 ? (size_t)p.nbs * s * rows * 128 * 4 : 0;  // one 32-bit word per partial value
+    p.fits = p.exchange_bytes <= kGemvExchangeBytes;
+    size_t off = shared_prefix_bytes(n);
     p.dummy_off = off;  // target of the stream's issues past a wave's last group (loaded, never used)
     off += kGemvDummyBytes;
-    p.partials_off = off;
-    if (s > 1) off += (size_t)p.nbs * s * rows * 128 * 8;  // generation-tagged fp32 partials
-    off = (off + 255) & ~(size_t)255;
     p.xpre_off = off;  // rows > 16: prepared activations of up to kGemvMaxTargets matrices
     if (rows > 16) off += (size_t)kGemvMaxTargets * p.kbs * gemv_frag_bytes_per_kb(rows);
     p.bytes = (off + 255) & ~(size_t)255;
     return p;
+}
+
+bool gemv_serves(size_t k, size_t n, size_t rows) {
+    return rows >= 1 && rows <= (size_t)kGemvMaxRows && gemv_plan(k, n, rows).fits;
 }
 
 template <int K, int CB>
@@ -552,21 +579,21 @@ static hipError_t launch_gemv_kc(const GemvTargets &tg, const void *x, int x_f16
     // x fastest: workgroup (nb, s) is dispatched as nb + s nbs, as a 1-D grid would be
     const dim3 grid((unsigned)p.nbs, (unsigned)p.splits), block(kGemvWaves * 64);
     const int kq = p.kbs / p.splits, kr = p.kbs % p.splits;
-    uint64_t *part = (uint64_t *)(ws + p.partials_off);
-    unsigned *cnt = (unsigned *)(ws + p.counters_off), *gens = (unsigned *)(ws + p.gens_off);
+    uint32_t *part = (uint32_t *)(ws + p.partials_off);
+    uint64_t *sync = (uint64_t *)(ws + p.counters_off);
     if (rows > 16) {
         uint16_t *xp = (uint16_t *)(ws + p.xpre_off);
         gemv_xprep_kernel<<<dim3((unsigned)((rows + 3) / 4), (unsigned)p.kbs, (unsigned)tg.count), dim3(256), 0,
                             stream>>>(tg, K, x, x_f16, x_stride, (int)rows, p.kbs, xp);
         gemv_kernel<K, CB, 2><<<grid, block, lds, stream>>>(tg, p.kbs, p.splits, kq, kr, x, x_f16, x_stride,
-                                                            (int)rows, ws + p.dummy_off, part, cnt, gens, y_f16,
+                                                            (int)rows, ws + p.dummy_off, part, sync, y_f16,
                                                             (const uint8_t *)xp);
     } else if (rows > 8) {
         gemv_kernel<K, CB, 1><<<grid, block, lds, stream>>>(tg, p.kbs, p.splits, kq, kr, x, x_f16, x_stride,
-                                                            (int)rows, ws + p.dummy_off, part, cnt, gens, y_f16, nullptr);
+                                                            (int)rows, ws + p.dummy_off, part, sync, y_f16, nullptr);
     } else {
         gemv_kernel<K, CB, 0><<<grid, block, lds, stream>>>(tg, p.kbs, p.splits, kq, kr, x, x_f16, x_stride,
-                                                            (int)rows, ws + p.dummy_off, part, cnt, gens, y_f16, nullptr);
+                                                            (int)rows, ws + p.dummy_off, part, sync, y_f16, nullptr);
     }
     return hipGetLastError();
 }

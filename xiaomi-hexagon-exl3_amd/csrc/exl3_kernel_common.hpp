@@ -29,54 +29,46 @@ __device__ __forceinline__ float mul_rn_f32(float a, float b) {
 }
 
 // Split-K hand-off through L2, without cache maintenance.  The partial sums of
-// a column group's k-splits cross XCDs (each XCD has its own L2): they are
-// written and read as 64-bit relaxed atomics at agent scope (sc1: coherent at
-// device scope), each value tagged with the column group's generation number.
-// Every workgroup bumps the group's arrival counter; the one that sees the
-// last count sums the partials, re-reading (boundedly) any word whose tag is
-// not yet the current generation, then advances the generation and clears the
-// counter for the next call.  Correctness rests only on the coherence of each
-// 64-bit word, so no release/acquire fence is needed; an agent-scope fence
-// would write back and invalidate the whole L2 on gfx950 (measured 14.6 ->
-// 53.8 us per call at k = 14336, n = 4096).  Waiting for the partial stores
-// before the counter bump keeps re-reads from happening in practice.
-constexpr int kTagSpinLimit = 1 << 20;
+// a column group's k-splits cross XCDs (each XCD has its own L2), through the
+// workspace's exchange: 32-bit words, zero ("empty") between calls.  Every
+// workgroup stores its partial there as relaxed agent-scope atomics (sc1:
+// coherent at device scope), each value complemented and never zero
+// (exchange_bits), then claims its arrival with a relaxed agent-scope fetch_add
+// on the column group's sync word.  The one that sees the last arrival count
+// sums the partials, reading again (in batches, boundedly) any word still
+// empty, then zeroes every word and the sync word, so the next call finds the
+// same state.  Within a call each word is zero or holds the value its one
+// writer stored, and 32-bit words are single-copy atomic: a nonzero word is
+// this call's value, whatever order the other words arrive in.  That is why no
+// release/acquire pair is needed; an agent-scope fence writes back or
+// invalidates the whole L2 on gfx950 (measured 14.6 -> 53.8 us per GEMV call at
+// k = 14336, n = 4096).  Writers wait for their stores to complete before they
+// claim, so in practice the last workgroup never reads a word twice.
+constexpr int kExchangeSpinLimit = 1 << 20;
 
-__device__ __forceinline__ unsigned load_relaxed(const unsigned *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void store_relaxed(unsigned *p, unsigned v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void store_tagged(uint64_t *p, float v, unsigned gen) {
-    __hip_atomic_store(p, (uint64_t)__float_as_uint(v) | (uint64_t)gen << 32, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t load_tagged(const uint64_t *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// the value of word p (first read w) once its tag is gen; NaN if it never
-// becomes so within kTagSpinLimit re-reads (a loud result, never a hang)
-__device__ __forceinline__ float tagged_value(const uint64_t *p, uint64_t w, unsigned gen) {
-    if ((unsigned)(w >> 32) != gen) {
-        int spin = 0;
-        do {
-            __builtin_amdgcn_s_sleep(1);
-            w = load_tagged(p);
-        } while ((unsigned)(w >> 32) != gen && ++spin < kTagSpinLimit);
-        if ((unsigned)(w >> 32) != gen) return __builtin_nanf("");
-    }
-    return __uint_as_float((uint32_t)w);
-}
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-// true in every thread of the last of `total` arriving workgroups
-__device__ __forceinline__ bool arrive_last(unsigned *counter, unsigned total, int *flag_lds) {
-    wait_stores();
-    __syncthreads();
-    if (threadIdx.x == 0)
-        *flag_lds = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == total - 1;
-    __syncthreads();
-    return *flag_lds != 0;
+__device__ __forceinline__ unsigned claim_arrival(uint64_t *sync) {  // arrivals before this one
+    return (unsigned)__hip_atomic_fetch_add((unsigned long long *)sync, 1ull, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void clear_sync(uint64_t *sync) {
+    __hip_atomic_store((unsigned long long *)sync, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// binary32 bits complemented; the one value whose complement is zero (the NaN
+// 0xffffffff) is stored as 1, which reads back as the NaN 0xfffffffe
+__device__ __forceinline__ uint32_t exchange_bits(float v) {
+    const uint32_t c = ~__float_as_uint(v);
+    return c ? c : 1u;
+}
+__device__ __forceinline__ float exchange_value(uint32_t w) { return __uint_as_float(~w); }
+__device__ __forceinline__ void store_exchange(uint32_t *p, float v) {
+    __hip_atomic_store(p, exchange_bits(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t load_exchange(const uint32_t *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void clear_exchange(uint32_t *p) {
+    __hip_atomic_store(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Tile address of trellis tile (rk, cn) of a k x n matrix.

@@ -23,9 +23,9 @@ std::mutex g_scratch_mutex;
 void *g_scratch_ptr[kMaxDevices];  // device address of `scratch` on each device, or null
 
 // The current device's scratch address.  On a device's first call the array's
-// split-K sync words (counters, generations) are cleared on `stream` with a fill
-// kernel (no hipMemsetAsync, so a first call under capture stays replay-safe);
-// every later call finds them zero again because each GEMV call resets them.
+// split-K sync words and exchange are cleared on `stream` with a fill kernel (no
+// hipMemsetAsync, so a first call under capture stays replay-safe); every later
+// call finds them zero again because each GEMV call leaves them so.
 exl3_status scratch_of_current_device(hipStream_t stream, void **out) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return EXL3_HIP_ERROR;
@@ -33,7 +33,7 @@ exl3_status scratch_of_current_device(hipStream_t stream, void **out) {
     if (!g_scratch_ptr[dev]) {
         void *p = nullptr;
         if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return EXL3_HIP_ERROR;
-        if (exl3k::launch_zero(p, exl3k::counter_region_bytes((size_t)exl3k::kCounterFloor * 128), stream) !=
+        if (exl3k::launch_zero(p, exl3k::shared_prefix_bytes((size_t)exl3k::kCounterFloor * 128), stream) !=
             hipSuccess)
             return EXL3_HIP_ERROR;
         g_scratch_ptr[dev] = p;
