@@ -117,34 +117,32 @@ def main():
     def call(i, rows, x):
         amd.mul_mat(copies[i % COPIES], BITS, K_IN, N_OUT, x, codebook=CB, y=ys[rows], workspace=ws[rows])
 
-    def capture(rows, x):
-        """One HIP graph holding COPIES launches, one per weight copy: replays
-        measure the kernels back to back, free of Python launch cost."""
+    def timed(rows, x, steps, warmup):
+        """Mean time of one layer call over exactly `steps` launches: `warmup`
+        untimed launches, then one HIP graph of `steps` launches (rotating through
+        the weight copies, free of Python launch cost) replayed once between HIP
+        events on the launch stream, synchronized on both sides."""
         for i in range(2):
             call(i, rows, x)
         torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for i in range(COPIES):
-                call(i, rows, x)
-        torch.cuda.synchronize()
-        return g
 
-    def timed(rows, x, steps, warmup):
-        """Average time of one layer call over >= steps launches (graph replays,
-        HIP events on the replay stream around the whole timed region)."""
-        g = capture(rows, x)
-        reps = max(1, -(-steps // COPIES))
-        for _ in range(max(1, -(-warmup // COPIES))):
-            g.replay()
+        def graph_of(count):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for i in range(count):
+                    call(i, rows, x)
+            return g
+
+        gw, gt = graph_of(max(1, warmup)), graph_of(steps)
+        torch.cuda.synchronize()
+        gw.replay()
         torch.cuda.synchronize()
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record(stream)
-        for _ in range(reps):
-            g.replay()
+        gt.replay()
         stop.record(stream)
         torch.cuda.synchronize()
-        return start.elapsed_time(stop) / (reps * COPIES), reps * COPIES
+        return start.elapsed_time(stop) / steps, steps
 
     if args.only_gemm:
         msg, n = timed(512, x512, max(36, args.steps // 2), max(18, args.warmup))
@@ -223,7 +221,7 @@ def main():
                    "k": K_IN, "n": N_OUT, "bits": BITS, "rows": 1, "weight_copies": COPIES},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "kernel": "exl3k::gemv_kernel<4,2,0>", "kernel_us_mean": round(ms1 * 1e3, 3),
+                     "kernel": "exl3k::gemv_kernel<4,2,0>", "us_per_launch": round(ms1 * 1e3, 3),
                      "algorithmic_bytes": b1},
         "cpu_baseline": cpu,
     }
@@ -385,7 +383,7 @@ def cpu_baseline(np, synth):
         return statistics.median(ts)
 
     t_all = med(cores, 5)
-    t_one = med(1, 3)
+    t_one = med(1, 5)
 
     # decode only (the CPU side of the dequant sweep): the oracle's decode_inner on
     # one MLP matrix, on one thread as the reference runs it, and in column slices
@@ -413,7 +411,7 @@ def cpu_baseline(np, synth):
         return statistics.median(ts)
 
     td_all = dec_med(cores, 5)
-    td_one = dec_med(1, 3)
+    td_one = dec_med(1, 5)
     cpu_model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -424,11 +422,12 @@ def cpu_baseline(np, synth):
         pass
     return {"value": round(b1 / t_all / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
             "sample": f"full k=14336 x n=4096 4-bpw layer, batch 1, oracle restatement of ggml_exl3_mul_mat, "
-                      f"{cores} threads (ggml nb partition), median of 5 after 1 warm-up; cpu {cpu_model}",
+                      f"{cores} threads (ggml nb partition) and 1 thread, median of 5 after 1 warm-up each; "
+                      f"cpu {cpu_model}",
             "ms": round(t_all * 1e3, 2), "single_thread_gbps": round(b1 / t_one / 1e9, 3),
             "single_thread_ms": round(t_one * 1e3, 1),
             "decode": {"sample": f"decode_inner restatement, k=2048 x n=6144 at 4 bits (one MLP matrix of the "
-                                 f"dequant sweep), {len(slices)} column slices on {cores} threads; median of 5 / 3",
+                                 f"dequant sweep), {len(slices)} column slices on {cores} threads; median of 5",
                        "gbps": round(dbytes / td_all / 1e9, 3), "ms": round(td_all * 1e3, 2),
                        "single_thread_gbps": round(dbytes / td_one / 1e9, 3),
                        "single_thread_ms": round(td_one * 1e3, 1)}}

@@ -135,6 +135,11 @@ exl3_status exl3_hip_workspace_init(void *workspace, size_t workspace_bytes, hip
  *   bits         1..8; codebook 0..2 (the reference's ggml op uses mul1 = 2)
  *   x            device, rows x k of xt, row stride x_row_stride elements (>= k)
  *   y            device, rows x n of yt, row stride y_row_stride elements (>= n)
+ *   input range  the kernels hold xh = H128(x[r] * su) / sqrt(128) in fp16 (as a
+ *                hi + lo pair up to 16 rows, hi only above), where the reference
+ *                keeps fp32: every element of xh must stay below 65520 in
+ *                magnitude (true whenever |x[r][i] * su[i]| <= 5790 for all i);
+ *                beyond that the affected output rows are Inf or NaN
  *   workspace    device, >= exl3_hip_mul_mat_workspace_bytes(k, n, rows), zero-filled
  *                before first use; NULL -> an internal per-(device, stream)
  *                workspace is allocated on first use and kept (grown, never

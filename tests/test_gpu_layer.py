@@ -407,3 +407,30 @@ def test_gemv_partials_beyond_exchange_run_as_gemm(amd):
     torch.cuda.synchronize()
     assert_layer_close(y32.cpu().numpy(), halves.cpu().numpy().astype(np.float64), what="GEMM fallback vs GEMV")
     assert int(torch.count_nonzero(ws[:SHARED_PREFIX])) == 0
+
+
+@pytest.mark.parametrize("rows", [1, 12, 20, 40])
+def test_fp32_input_range(amd, oracle, rows):
+    """fp32 activations up to the documented range (|x su| <= 5790 keeps the fp16
+    xh = H128(x su)/sqrt(128) finite): sigma 1000 (|x| up to ~5000) matches the
+    oracle within the layer tolerance, scaled to the output size, on the GEMV's hi/lo
+    path (rows 1, 12), its fp16 path (20) and the GEMM (40).  Far beyond the range
+    (sigma 1e6) the affected rows are not finite, as documented."""
+    import torch
+    k, n, bits = 1024, 384, 4
+    rec = make_layer(1600, k, n, bits)
+    rd = dev(rec)
+    rng = np.random.default_rng(1601 + rows)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    big = x * np.float32(1000.0)
+    big = np.clip(big, -5790.0, 5790.0).astype(np.float32)
+    y = run(amd, rd, bits, k, n, big)
+    ref = oracle.mul_mat(rec, bits, 2, k, n, big)
+    scale = float(np.max(np.abs(ref)))
+    ma, rl = layer_stats(y, ref)
+    print(f"  fp32 range rows={rows}: max_abs={ma:.3e} (output scale {scale:.1f}) rel_l2={rl:.3e}", flush=True)
+    assert np.all(np.isfinite(y))
+    assert rl <= 1e-3 and ma <= 1e-2 * max(1.0, scale / 10.0)
+    huge = (x * np.float32(1e6)).astype(np.float32)
+    yh = run(amd, rd, bits, k, n, huge)
+    assert not np.all(np.isfinite(yh))
