@@ -151,7 +151,7 @@ size_t exl3_hip_mul_mat_workspace_bytes(size_t k, size_t n, size_t rows) {
     // m-tile count within it
     for (size_t r = exl3k::kGemvMaxRows + 1; r <= rows;) {
         const size_t bm = (size_t)exl3k::gemm_tile_rows(r);
-        const size_t class_end = bm == 128 ? 128 : rows;
+        const size_t class_end = bm < 512 ? bm : rows;
         const size_t r_hi = std::min(rows, std::min(class_end, (r + bm - 1) / bm * bm));
         need = std::max(need, exl3k::gemm_plan(k, n, r_hi).bytes);
         r = r_hi + 1;

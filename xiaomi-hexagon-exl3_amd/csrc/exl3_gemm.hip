@@ -117,28 +117,29 @@ __global__ __launch_bounds__(256) void gemm_xprep_kernel(const uint8_t *__restri
     }
 }
 
-// GEMM (rows > 32).  Workgroup (split s, m-tile mt, column group nb): rows
-// [BM mt, +BM) x columns [128 nb, +128), records kb in [kb0, kb1); BM = 64 RB
-// rows, wave w owning rows 32 RB w .. +32 RB for all 128 columns: RB x 4
-// accumulator blocks of v_mfma_f32_32x32x16_f16 (one wave per SIMD keeps this
-// MFMA at full rate; the 16x16 one needs two).  Per record kb, software-pipelined
-// in straight-line code per k-step (16 k):
+// GEMM (rows > 32).  Workgroup (split s, m-tile mt, column group nb) of W waves
+// (4 or 8): rows [BM mt, +BM) x columns [128 nb, +128), records kb in [kb0, kb1);
+// BM = 32 RB W rows, wave w owning rows 32 RB w .. +32 RB for all 128 columns:
+// RB x 4 accumulator blocks of v_mfma_f32_32x32x16_f16 (one wave per SIMD keeps
+// this MFMA at full rate; the 16x16 one needs two).  Per record kb,
+// software-pipelined in straight-line code per k-step (16 k):
 //   * MFMAs of k-step ks (A = activations, B = decoded weights), the B fragments
 //     of k-step ks + 1 already being read from LDS;
-//   * one eighth of the decode of record kb + 1 (fragment ks / 2 of the wave's
-//     chunk ks % 2: the GEMV's chunk decoder) into the other LDS buffer W[n][k]
-//     (fp16, 16-byte k-chunks XOR-swizzled by n % 16: conflict-free MFMA B
-//     reads), interleaved with the MFMAs;
-//   * the activations of k-step ks of record kb + 1 (xh16, fragment-tiled and
-//     L2-resident: every column group reads it), into the registers just consumed.
+//   * a share of the decode of record kb + 1 (each wave decodes H = 8 / W of the
+//     record's eight trellis chunks with the GEMV's chunk decoder, one fragment
+//     per k-step or every other k-step) into the other LDS buffer W[n][k] (fp16,
+//     16-byte k-chunks XOR-swizzled by n % 16: conflict-free MFMA B reads),
+//     interleaved with the MFMAs;
+//   * the activations of k-step ks + XD (xh16, fragment-tiled and L2-resident:
+//     every column group reads it), into the registers just consumed.
 // The weight words are loaded two records ahead.  MFMA 32x32x16 operands: A lane l
 // = row l % 32, k 8 (l / 32) + j; B lane l = column l % 32, k 8 (l / 32) + j;
 // D element e of lane l = row (e % 4) + 8 (e / 4) + 4 (l / 32), column l % 32.
-// Split-K partials (kept in the accumulator layout) are summed in split order by
-// the last workgroup of the tile, which applies H128 over the 128 columns of
-// each row in registers (strides 1..16: lanes, 32 and 64: blocks) and sv
-// (src/exl3-ggml.cpp:84-90).
-constexpr int kGemmTargetWgs = 256;  // one 4-wave workgroup per CU (the accumulators fill the register file)
+// Without a k split the workgroup applies H128 over the 128 columns of each row
+// in registers (strides 1..16: lanes, 32 and 64: blocks) and sv
+// (src/exl3-ggml.cpp:84-90); with one, gemm_reduce_kernel sums the partials in
+// split order and does the same.
+constexpr int kGemmTargetWgs = 256;  // one workgroup per CU (the accumulators fill the register file)
 
 __device__ __forceinline__ int gemm_w_offset(int n, int chunk) {  // halves
     return n * 128 + ((chunk ^ (n & 15)) << 3);
@@ -229,12 +230,13 @@ __device__ __forceinline__ void gemm_rows_out(float (&t)[4][NE], int lane, int r
     }
 }
 
-template <int K, int CB, int RB>
-__global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
+template <int K, int CB, int RB, int W, int NSG, int XD>
+__global__ __launch_bounds__(W * 64) void gemm_kernel(
     const uint8_t *__restrict__ records, int kbs, int nbs, int mtiles, int splits, int kq, int kr,
-    const uint16_t *__restrict__ xh16, size_t k, uint16_t *__restrict__ partials, void *y, int y_f16, size_t y_stride,
-    int rows, const void *res, size_t res_stride) {
-    constexpr int BM = 32 * RB * kGemmWaves;
+    const uint16_t *__restrict__ xh16, size_t k, uint16_t *__restrict__ partials, int *__restrict__ exps, void *y,
+    int y_f16, size_t y_stride, int rows, const void *res, size_t res_stride) {
+    constexpr int BM = 32 * RB * W;
+    constexpr int H = 8 / W;  // trellis chunks a wave decodes per record
     constexpr size_t GB = (size_t)2048 * K + 512;
     __shared__ __attribute__((aligned(16))) uint16_t wlds[2][128 * 128];  // 64 KB
 
@@ -257,26 +259,25 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
     const int kb0 = s * kq + (s < kr ? s : kr), kb1 = kb0 + kq + (s < kr ? 1 : 0);
     const uint8_t *colgroup = records + (size_t)nb * kbs * GB;
 
-    // weights: this wave decodes groups q = 2 wave + h (h = 0, 1) of every record
-    uint32_t wlane[2];
-    int wn0[2], wc0[2];  // column and k-chunk of fragment 0 of each chunk
+    // weights: this wave decodes groups q = H wave + h (h < H) of every record
+    uint32_t wlane[H];
+    int wn0[H], wc0[H];  // column and k-chunk of fragment 0 of each chunk
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int q = 2 * wave + h, r4 = q >> 2, c2 = q & 3;
+    for (int h = 0; h < H; ++h) {
+        const int q = H * wave + h, r4 = q >> 2, c2 = q & 3;
         wlane[h] = (uint32_t)(r4 * 1024 * K + ((8 * lg + 2 * c2 + (li >> 3)) * 32 + 4 * j) * K);
         wn0[h] = 16 * (2 * c2 + (li >> 3)) + j;
         wc0[h] = 2 * (4 * r4 + lg);
     }
-    auto load_words = [&](int kb, uint32_t (&w)[2][K]) {
+    auto load_words = [&](int kb, uint32_t (&w)[H][K]) {
         const uint8_t *rec = colgroup + (size_t)(kb < kb1 ? kb : kb1 - 1) * GB;  // past the end: re-read, unused
-        load_chunk<K>(rec + wlane[0], w[0]);
-        load_chunk<K>(rec + wlane[1], w[1]);
+#pragma unroll
+        for (int h = 0; h < H; ++h) load_chunk<K>(rec + wlane[h], w[h]);
     };
     const bool first_chunk = j == 0;
-    // boundary words of the two chunks (see decode_chunk), for the pieces below
-    auto chunk_prepare = [&](const uint32_t (&w)[2][K], uint32_t (&xb)[2][K]) {
+    auto chunk_prepare = [&](const uint32_t (&w)[H][K], uint32_t (&xb)[H][K]) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < H; ++h) {
             const uint32_t p1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)w[h][K - 1], 0x121, 0xF, 0xF, false);
             const uint32_t p9 = (uint32_t)__builtin_amdgcn_mov_dpp((int)w[h][K - 1], 0x129, 0xF, 0xF, false);
             xb[h][0] = __builtin_amdgcn_alignbit(first_chunk ? p9 : p1, w[h][0], 16);
@@ -284,10 +285,10 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
             for (int m = 1; m < K; ++m) xb[h][m] = __builtin_amdgcn_alignbit(w[h][m - 1], w[h][m], 16);
         }
     };
-    // piece P: fragment F = P / 2 of chunk h = P % 2 -> LDS at column
-    // n0 + 8 (F >> 1), k-chunk c0 + (F & 1)
-    auto decode_piece = [&](auto pc, const uint32_t (&w)[2][K], const uint32_t (&xb)[2][K], uint16_t *dst) {
-        constexpr int F = decltype(pc)::value >> 1, h = decltype(pc)::value & 1;
+    // piece P (0 .. 4 H - 1): fragment F = P / H of chunk h = P % H -> LDS at
+    // column n0 + 8 (F >> 1), k-chunk c0 + (F & 1)
+    auto decode_piece = [&](auto pc, const uint32_t (&w)[H][K], const uint32_t (&xb)[H][K], uint16_t *dst) {
+        constexpr int F = decltype(pc)::value / H, h = decltype(pc)::value % H;
         const u4 fr = chunk_frag<K, CB, F>(w[h], xb[h]);
         *(u4 *)(dst + gemm_w_offset(wn0[h] + 8 * (F >> 1), wc0[h] + (F & 1))) = fr;
     };
@@ -325,10 +326,10 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
 
     // prologue: words of kb0 and kb0 + 1, activations of kb0, record kb0 decoded,
     // B fragments of its first k-step
-    uint32_t wbuf[2][2][K], xb[2][K];
-    h8 xa[8][RB];
+    uint32_t wbuf[2][H][K], xb[H][K];
+    h8 xa[XD][RB];
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) load_x_step(kb0, ks, xa[ks]);
+    for (int ks = 0; ks < XD; ++ks) load_x_step(kb0, ks, xa[ks]);
     load_words(kb0, wbuf[0]);
     load_words(kb0 + 1, wbuf[1]);
     chunk_prepare(wbuf[0], xb);
@@ -336,29 +337,32 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
     decode_piece(std::integral_constant<int, 1>{}, wbuf[0], xb, wlds[0]);
     decode_piece(std::integral_constant<int, 2>{}, wbuf[0], xb, wlds[0]);
     decode_piece(std::integral_constant<int, 3>{}, wbuf[0], xb, wlds[0]);
-    decode_piece(std::integral_constant<int, 4>{}, wbuf[0], xb, wlds[0]);
-    decode_piece(std::integral_constant<int, 5>{}, wbuf[0], xb, wlds[0]);
-    decode_piece(std::integral_constant<int, 6>{}, wbuf[0], xb, wlds[0]);
-    decode_piece(std::integral_constant<int, 7>{}, wbuf[0], xb, wlds[0]);
+    if constexpr (H == 2) {
+        decode_piece(std::integral_constant<int, 4>{}, wbuf[0], xb, wlds[0]);
+        decode_piece(std::integral_constant<int, 5>{}, wbuf[0], xb, wlds[0]);
+        decode_piece(std::integral_constant<int, 6>{}, wbuf[0], xb, wlds[0]);
+        decode_piece(std::integral_constant<int, 7>{}, wbuf[0], xb, wlds[0]);
+    }
     __syncthreads();
     h8 bc[4], bn[4];
     read_b(wlds[0], 0, bc);
 
     // one k-step: B of ks + 1 requested, MFMAs of ks, a decode piece, then the
     // activations of ks for the next record
-    auto kstep = [&](auto kc, int kb, const uint16_t *wcur, uint16_t *wnext, const uint32_t (&wnextw)[2][K],
+    auto kstep = [&](auto kc, int kb, const uint16_t *wcur, uint16_t *wnext, const uint32_t (&wnextw)[H][K],
                      h8 (&bcur)[4], h8 (&bnxt)[4]) {
         constexpr int KS = decltype(kc)::value;
         if constexpr (KS < 7) read_b(wcur, KS + 1, bnxt);
-        mma_step(xa[KS], bcur);
-        decode_piece(std::integral_constant<int, KS>{}, wnextw, xb, wnext);
-        load_x_step(kb + 1, KS, xa[KS]);
+        mma_step(xa[KS % XD], bcur);
+        if constexpr (H == 2) decode_piece(std::integral_constant<int, KS>{}, wnextw, xb, wnext);
+        else if constexpr (KS % 2 == 0) decode_piece(std::integral_constant<int, KS / 2>{}, wnextw, xb, wnext);
+        load_x_step(KS + XD < 8 ? kb : kb + 1, (KS + XD) % 8, xa[KS % XD]);
         // One MFMA every few VALU instructions: the wave issues in order, so
         // MFMAs back to back stall it while the decode waits behind them.  The
         // B reads lead, the activation loads (seven k-steps ahead of their use:
         // left alone the scheduler sinks them to the end of the record) trail.
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < NSG; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
             if (i < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
             __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);  // VALU
@@ -369,8 +373,8 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
     };
     // record kb: activations xa, decoded weights wcur (B fragments of k-step 0 in
     // bc); words of kb + 1 in wnextw; slot wfree takes the words of kb + 2
-    auto step = [&](int kb, const uint16_t *wcur, uint16_t *wnext, uint32_t (&wfree)[2][K],
-                    const uint32_t (&wnextw)[2][K]) {
+    auto step = [&](int kb, const uint16_t *wcur, uint16_t *wnext, uint32_t (&wfree)[H][K],
+                    const uint32_t (&wnextw)[H][K]) {
         load_words(kb + 2, wfree);
         chunk_prepare(wnextw, xb);
         kstep(std::integral_constant<int, 0>{}, kb, wcur, wnext, wnextw, bc, bn);
@@ -393,9 +397,11 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
 #pragma unroll
         for (int ks = 0; ks < 8; ks += 2) {
             read_b(wlds[0], ks + 1, bn);
-            mma_step(xa[ks], bc);
+            mma_step(xa[ks % XD], bc);
+            if (ks + XD < 8) load_x_step(kb, ks + XD, xa[ks % XD]);
             if (ks + 2 < 8) read_b(wlds[0], ks + 2, bc);
-            mma_step(xa[ks + 1], bn);
+            mma_step(xa[(ks + 1) % XD], bn);
+            if (ks + 1 + XD < 8) load_x_step(kb, ks + 1 + XD, xa[(ks + 1) % XD]);
         }
     }
 
@@ -404,25 +410,38 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
     if (splits > 1) {
         // fp16 partials in accumulator layout [tile][split][wave][rb][cb][vp][lane]
         // x 16 bytes: elements 8 vp .. 8 vp + 7 of acc[rb][cb] (rows of v = 2 vp,
-        // 2 vp + 1), summed in fp32 by gemm_reduce_kernel.  fp16 keeps the layer
-        // within its tolerance (rel-L2 2.9e-4 against 2.1e-4 for fp32 partials
-        // with fp16 output, at k = 14336) for half the bytes.
-        constexpr size_t kPerSplit = (size_t)kGemmWaves * RB * 4 * 2 * 64 * 8;  // halves
+        // 2 vp + 1), summed in fp32 by gemm_reduce_kernel.  Each (wave, rb) block
+        // is stored scaled by 2^-e, e = exps[(tile, split, wave, rb)] chosen so that
+        // its largest magnitude is below 2^14: fp16's relative precision for every
+        // value, and no overflow however large the activations.  fp16 keeps the
+        // layer within its tolerance (rel-L2 2.9e-4 against 2.1e-4 for fp32
+        // partials with fp16 output, at k = 14336) for half the bytes.
+        constexpr size_t kPerSplit = (size_t)W * RB * 4 * 2 * 64 * 8;  // halves
         uint16_t *dst = partials + ((size_t)tile * splits + s) * kPerSplit + (size_t)wave * RB * 8 * 512 + lane * 8;
-        auto pk = [](float a, float b) {
-            return (uint32_t)float_to_half_bits(a) | ((uint32_t)float_to_half_bits(b) << 16);
+        auto pk = [](float a, float b, int e) {
+            return (uint32_t)float_to_half_bits(__builtin_amdgcn_ldexpf(a, -e)) |
+                   ((uint32_t)float_to_half_bits(__builtin_amdgcn_ldexpf(b, -e)) << 16);
         };
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
+        for (int rb = 0; rb < RB; ++rb) {
+            float m = 0.f;
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) m = fmaxf(m, fabsf(acc[rb][cb][e]));
+            m = wave_max(m);
+            const int ex = __builtin_amdgcn_frexp_expf(m) - 14;  // m < 2^(ex + 14); 0 (and Inf, NaN): -14
+            if (lane == 0) exps[((size_t)tile * splits + s) * (W * RB) + wave * RB + rb] = ex;
 #pragma unroll
             for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
                 for (int vp = 0; vp < 2; ++vp) {
                     const f16v &a = acc[rb][cb];
-                    const u4 d = {pk(a[8 * vp], a[8 * vp + 1]), pk(a[8 * vp + 2], a[8 * vp + 3]),
-                                  pk(a[8 * vp + 4], a[8 * vp + 5]), pk(a[8 * vp + 6], a[8 * vp + 7])};
+                    const u4 d = {pk(a[8 * vp], a[8 * vp + 1], ex), pk(a[8 * vp + 2], a[8 * vp + 3], ex),
+                                  pk(a[8 * vp + 4], a[8 * vp + 5], ex), pk(a[8 * vp + 6], a[8 * vp + 7], ex)};
                     __builtin_nontemporal_store(d, (u4 *)(dst + ((rb * 4 + cb) * 2 + vp) * 512));
                 }
+        }
         return;
     }
     const uint16_t *svp = (const uint16_t *)(colgroup + 2048 * K + 256);  // record (nb, 0)
@@ -443,26 +462,29 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(
 // (fp16) of every split in fp32 in split order (so the result does not depend on
 // the order the GEMM's workgroups ran in), then H128, 1/sqrt(128) and sv over its
 // 16 rows.
-template <int RB>
-__global__ __launch_bounds__(256) void gemm_reduce_kernel(const uint16_t *__restrict__ partials, int splits, int nbs,
+template <int RB, int W>
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(const uint16_t *__restrict__ partials,
+                                                          const int *__restrict__ exps, int splits, int nbs,
                                                           const uint8_t *__restrict__ records, int bits, int kbs,
                                                           void *y, int y_f16, size_t y_stride, int rows,
                                                           int nwaves, const void *res, size_t res_stride) {
-    constexpr int BM = 32 * RB * kGemmWaves;
-    constexpr size_t kPerSplit = (size_t)kGemmWaves * RB * 4 * 2 * 64 * 8;  // halves
+    constexpr int BM = 32 * RB * W;
+    constexpr size_t kPerSplit = (size_t)W * RB * 4 * 2 * 64 * 8;  // halves
     const int lane = threadIdx.x & 63;
     const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (gw >= nwaves) return;
-    const int vp = gw & 1, blk = (gw >> 1) % (kGemmWaves * RB), tile = (gw >> 1) / (kGemmWaves * RB);
+    const int vp = gw & 1, blk = (gw >> 1) % (W * RB), tile = (gw >> 1) / (W * RB);
     const int mt = tile / nbs, nb = tile - mt * nbs;
     const uint16_t *src = partials + (size_t)tile * splits * kPerSplit + (size_t)blk * 8 * 512 + vp * 512 + lane * 8;
     float t[4][8];
 #pragma unroll 1
     for (int sp0 = 0; sp0 < splits; sp0 += 4) {  // loads of four splits in flight, then their sum in order
         u4 in[4][4];
+        int ex[4];  // each split's block exponent (the GEMM stored the block scaled by 2^-ex)
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int sp = sp0 + u < splits ? sp0 + u : splits - 1;
+            ex[u] = exps[((size_t)tile * splits + sp) * (W * RB) + blk];
 #pragma unroll
             for (int cb = 0; cb < 4; ++cb) in[u][cb] = *(const u4 *)(src + (size_t)sp * kPerSplit + cb * 2 * 512);
         }
@@ -474,7 +496,8 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const uint16_t *__rest
                     const uint32_t w[4] = {in[u][cb].x, in[u][cb].y, in[u][cb].z, in[u][cb].w};
 #pragma unroll
                     for (int q = 0; q < 8; ++q) {
-                        const float v = half_bits_to_float((uint16_t)(w[q >> 1] >> (16 * (q & 1))));
+                        const float v =
+                            __builtin_amdgcn_ldexpf(half_bits_to_float((uint16_t)(w[q >> 1] >> (16 * (q & 1)))), ex[u]);
                         t[cb][q] = sp0 + u == 0 ? v : t[cb][q] + v;
                     }
                 }
@@ -484,7 +507,10 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const uint16_t *__rest
                      res_stride);
 }
 
-int gemm_tile_rows(size_t rows) { return rows <= 128 ? 128 : 256; }
+// Tile heights: 128 rows (4 waves, one 32-row block each), 256 (4 waves, two
+// blocks), 512 (8 waves, two blocks): above 256 rows one 512-row tile decodes each
+// record once for all rows where two 256-row tiles decode it twice.
+int gemm_tile_rows(size_t rows) { return rows <= 128 ? 128 : rows <= 256 ? 256 : 512; }
 
 GemmPlan gemm_plan(size_t k, size_t n, size_t rows) {
     GemmPlan p{};
@@ -505,32 +531,42 @@ GemmPlan gemm_plan(size_t k, size_t n, size_t rows) {
     off += ((size_t)p.mtiles * p.bm * k * 2 + 255) & ~(size_t)255;
     p.partials_off = off;
     if (s > 1) off += (size_t)tiles * s * p.bm * 128 * 2;  // fp16 partials
+    p.exps_off = off;
+    if (s > 1) off += ((size_t)tiles * s * (p.bm / 32) * 4 + 255) & ~(size_t)255;  // one exponent per 32-row block
     p.bytes = (off + 255) & ~(size_t)255;
     return p;
+}
+
+// one tile class: kernel <RB, W> (NSG scheduling groups per k-step, XD activation
+// k-steps in flight) and its reduction
+template <int K, int CB, int RB, int W, int NSG, int XD>
+static void launch_gemm_tiles(const uint8_t *rec, size_t k, uint16_t *xh, size_t rows, void *y, int y_f16,
+                              size_t y_stride, uint8_t *ws, const GemmPlan &p, hipStream_t stream, const void *res,
+                              size_t res_stride) {
+    const dim3 grid((unsigned)(p.mtiles * p.nbs * p.splits)), block(W * 64);
+    static_assert(32 * RB * W == 128 || 32 * RB * W == 256 || 32 * RB * W == 512, "tile height");
+    uint16_t *part = (uint16_t *)(ws + p.partials_off);
+    int *exps = (int *)(ws + p.exps_off);
+    const int nwaves = p.mtiles * p.nbs * (p.bm / 16);  // reduction: one wave per 16 rows of a tile
+    const int kq = p.kbs / p.splits, kr = p.kbs % p.splits;
+    gemm_kernel<K, CB, RB, W, NSG, XD><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, kq, kr, xh,
+                                                                   k, part, exps, y, y_f16, y_stride, (int)rows, res,
+                                                                   res_stride);
+    if (p.splits > 1)
+        gemm_reduce_kernel<RB, W><<<dim3((unsigned)((nwaves + 3) / 4)), dim3(256), 0, stream>>>(
+            part, exps, p.splits, p.nbs, rec, K, p.kbs, y, y_f16, y_stride, (int)rows, nwaves, res, res_stride);
 }
 
 template <int K, int CB>
 static void launch_gemm_kc(const uint8_t *rec, size_t k, uint16_t *xh, size_t rows, void *y, int y_f16,
                            size_t y_stride, uint8_t *ws, const GemmPlan &p, hipStream_t stream, const void *res,
                            size_t res_stride) {
-    const dim3 grid((unsigned)(p.mtiles * p.nbs * p.splits)), block(kGemmWaves * 64);
-    uint16_t *part = (uint16_t *)(ws + p.partials_off);
-    const int nwaves = p.mtiles * p.nbs * (p.bm / 16);  // reduction: one wave per 16 rows of a tile
-    const int kq = p.kbs / p.splits, kr = p.kbs % p.splits;
-    const dim3 rgrid((unsigned)((nwaves + 3) / 4));
-    if (p.bm == 128) {
-        gemm_kernel<K, CB, 1><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, kq, kr, xh, k, part,
-                                                          y, y_f16, y_stride, (int)rows, res, res_stride);
-        if (p.splits > 1)
-            gemm_reduce_kernel<1><<<rgrid, dim3(256), 0, stream>>>(part, p.splits, p.nbs, rec, K, p.kbs, y, y_f16,
-                                                                   y_stride, (int)rows, nwaves, res, res_stride);
-    } else {
-        gemm_kernel<K, CB, 2><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, kq, kr, xh, k, part,
-                                                          y, y_f16, y_stride, (int)rows, res, res_stride);
-        if (p.splits > 1)
-            gemm_reduce_kernel<2><<<rgrid, dim3(256), 0, stream>>>(part, p.splits, p.nbs, rec, K, p.kbs, y, y_f16,
-                                                                   y_stride, (int)rows, nwaves, res, res_stride);
-    }
+    if (p.bm == 128)
+        launch_gemm_tiles<K, CB, 1, 4, 8, 8>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream, res, res_stride);
+    else if (p.bm == 256)
+        launch_gemm_tiles<K, CB, 2, 4, 8, 8>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream, res, res_stride);
+    else  // 8 waves: no scheduling groups, four activation k-steps in flight (measured best at M = 512)
+        launch_gemm_tiles<K, CB, 2, 8, 0, 4>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream, res, res_stride);
 }
 
 template <int K>

@@ -71,6 +71,16 @@ __device__ __forceinline__ void clear_exchange(uint32_t *p) {
     __hip_atomic_store(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// maximum of v over the wave, in every lane
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_xor<1>(v));
+    v = fmaxf(v, dpp_xor<2>(v));
+    v = fmaxf(v, dpp_xor<4>(v));
+    v = fmaxf(v, dpp_xor<8>(v));
+    v = fmaxf(v, __shfl_xor(v, 16));
+    return fmaxf(v, __shfl_xor(v, 32));
+}
+
 // Tile address of trellis tile (rk, cn) of a k x n matrix.
 template <int K>
 __device__ __forceinline__ const uint32_t *tile_ptr(const uint8_t *src, int records_layout, size_t k, size_t n,

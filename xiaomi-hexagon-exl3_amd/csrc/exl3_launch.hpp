@@ -13,7 +13,6 @@ namespace exl3k {
 // up to 16); 17..32 rows as two blocks of 16 fp16 rows prepared once per call
 constexpr int kGemvMaxRows = 32;
 constexpr int kGemvWaves = 8;     // waves per GEMV workgroup (a multiple of 4)
-constexpr int kGemmWaves = 4;
 
 // Every plan starts with the same two regions, which only the GEMV's split-K
 // hand-off touches:
@@ -67,8 +66,8 @@ struct GemvPlan {
     bool fits;  // the partials fit the exchange (else the call runs as a GEMM)
 };
 struct GemmPlan {
-    int nbs, kbs, bm, mtiles, splits;  // bm: rows per workgroup tile (128 or 256)
-    size_t counters_off, xh_off, partials_off, bytes;
+    int nbs, kbs, bm, mtiles, splits;  // bm: rows per workgroup tile (128, 256 or 512)
+    size_t counters_off, xh_off, partials_off, exps_off, bytes;
 };
 
 GemvPlan gemv_plan(size_t k, size_t n, size_t rows);
