@@ -48,6 +48,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-gemv", action="store_true", help="headline GEMV only (for profiling)")
     ap.add_argument("--only-gemm", action="store_true", help="M=512 GEMM only (for profiling)")
+    ap.add_argument("--only-c1", action="store_true", help="the k=2048 x n=6144 batch-1 GEMV only (for profiling)")
     ap.add_argument("--no-extra", action="store_true", help="skip the C1/C2/C4/GET_ROWS lines")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only time a plain device copy of COPY_BYTES (scales the HBM byte counters)")
@@ -100,6 +101,9 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream()
+    if args.only_c1:
+        print(json.dumps(extra_configs(amd, torch, np, synth, stream, args, only_c1=True)), flush=True)
+        return
 
     # ---- synthetic layer, 18 resident copies
     p = synth.packed_tiles(77, K_IN, N_OUT, BITS)
@@ -259,7 +263,7 @@ def graph_time(torch, stream, fn, per_graph, replays=3):
     return s_ev.elapsed_time(e_ev) / (replays * per_graph)
 
 
-def extra_configs(amd, torch, np, synth, stream, args):
+def extra_configs(amd, torch, np, synth, stream, args, only_c1=False):
     out = {}
     dev = torch.device("cuda", 0)
     g = torch.Generator(device=dev)
@@ -288,6 +292,8 @@ def extra_configs(amd, torch, np, synth, stream, args):
                                          algo_bytes(k, n, bits, 1) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
                                      "note": "graph replay, 48 weight copies"}
     del copies
+    if only_c1:
+        return out
 
     # C4: projection set of one decoder layer at batch 8, mixed bits, x ~ N(0, sigma 0.5)
     proj = [("q", 2048, 2048, 6), ("k", 2048, 512, 6), ("v", 2048, 512, 6), ("o", 2048, 2048, 6),

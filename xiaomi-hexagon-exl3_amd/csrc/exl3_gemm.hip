@@ -477,19 +477,22 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const uint16_t *__rest
     const int mt = tile / nbs, nb = tile - mt * nbs;
     const uint16_t *src = partials + (size_t)tile * splits * kPerSplit + (size_t)blk * 8 * 512 + vp * 512 + lane * 8;
     float t[4][8];
+    // loads of eight splits in flight, then their sum in order (one wave per SIMD:
+    // registers are not what limits this kernel, round trips are)
+    constexpr int SB = 8;
 #pragma unroll 1
-    for (int sp0 = 0; sp0 < splits; sp0 += 4) {  // loads of four splits in flight, then their sum in order
-        u4 in[4][4];
-        int ex[4];  // each split's block exponent (the GEMM stored the block scaled by 2^-ex)
+    for (int sp0 = 0; sp0 < splits; sp0 += SB) {
+        u4 in[SB][4];
+        int ex[SB];  // each split's block exponent (the GEMM stored the block scaled by 2^-ex)
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < SB; ++u) {
             const int sp = sp0 + u < splits ? sp0 + u : splits - 1;
             ex[u] = exps[((size_t)tile * splits + sp) * (W * RB) + blk];
 #pragma unroll
             for (int cb = 0; cb < 4; ++cb) in[u][cb] = *(const u4 *)(src + (size_t)sp * kPerSplit + cb * 2 * 512);
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < SB; ++u)
             if (sp0 + u < splits)
 #pragma unroll
                 for (int cb = 0; cb < 4; ++cb) {
