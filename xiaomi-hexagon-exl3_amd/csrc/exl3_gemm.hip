@@ -457,57 +457,89 @@ __global__ __launch_bounds__(W * 64) void gemm_kernel(
     }
 }
 
-// Split-K reduction (split count > 1): one wave per (tile, row block blk =
-// RB wave + rb, vp) of the GEMM's partial layout; lane l sums its 4 x 16 bytes
-// (fp16) of every split in fp32 in split order (so the result does not depend on
-// the order the GEMM's workgroups ran in), then H128, 1/sqrt(128) and sv over its
-// 16 rows.
+// Split-K reduction (split count > 1).  One workgroup of 4 waves per unit
+// (tile, row block blk = RB wave + rb, vp): the 16 rows 32 blk + 16 vp .. +15 of
+// the tile x its 128 columns.  Wave c sums column block c (32 columns) over the
+// splits in fp32 in split order (so the result does not depend on the order the
+// GEMM's workgroups ran in): per split one 16-byte load per lane, all of a batch
+// in flight together; the sums go through LDS as [row][column], and wave w then
+// finishes rows 4 w .. 4 w + 3 (h128_wave over the 128 columns, sv, the optional
+// residual), lane l writing columns l and l + 64.
 template <int RB, int W>
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(const uint16_t *__restrict__ partials,
                                                           const int *__restrict__ exps, int splits, int nbs,
                                                           const uint8_t *__restrict__ records, int bits, int kbs,
-                                                          void *y, int y_f16, size_t y_stride, int rows,
-                                                          int nwaves, const void *res, size_t res_stride) {
+                                                          void *y, int y_f16, size_t y_stride, int rows, int nunits,
+                                                          const void *res, size_t res_stride) {
     constexpr int BM = 32 * RB * W;
     constexpr size_t kPerSplit = (size_t)W * RB * 4 * 2 * 64 * 8;  // halves
-    const int lane = threadIdx.x & 63;
-    const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (gw >= nwaves) return;
-    const int vp = gw & 1, blk = (gw >> 1) % (W * RB), tile = (gw >> 1) / (W * RB);
+    __shared__ float sums[16][129];  // [row][column], padded against bank conflicts
+    const int lane = threadIdx.x & 63, c = threadIdx.x >> 6;
+    const int u = blockIdx.x;
+    if (u >= nunits) return;  // whole workgroups
+    const int vp = u & 1, blk = (u >> 1) % (W * RB), tile = (u >> 1) / (W * RB);
     const int mt = tile / nbs, nb = tile - mt * nbs;
-    const uint16_t *src = partials + (size_t)tile * splits * kPerSplit + (size_t)blk * 8 * 512 + vp * 512 + lane * 8;
-    float t[4][8];
-    // loads of eight splits in flight, then their sum in order (one wave per SIMD:
-    // registers are not what limits this kernel, round trips are)
-    constexpr int SB = 8;
+    const uint16_t *src = partials + (size_t)tile * splits * kPerSplit + (size_t)blk * 8 * 512 + (c * 2 + vp) * 512 +
+                          lane * 8;
+    float t[8];
+    constexpr int SB = 8;  // splits' loads in flight
 #pragma unroll 1
     for (int sp0 = 0; sp0 < splits; sp0 += SB) {
-        u4 in[SB][4];
+        u4 in[SB];
         int ex[SB];  // each split's block exponent (the GEMM stored the block scaled by 2^-ex)
 #pragma unroll
-        for (int u = 0; u < SB; ++u) {
-            const int sp = sp0 + u < splits ? sp0 + u : splits - 1;
-            ex[u] = exps[((size_t)tile * splits + sp) * (W * RB) + blk];
-#pragma unroll
-            for (int cb = 0; cb < 4; ++cb) in[u][cb] = *(const u4 *)(src + (size_t)sp * kPerSplit + cb * 2 * 512);
+        for (int q = 0; q < SB; ++q) {
+            const int sp = sp0 + q < splits ? sp0 + q : splits - 1;
+            ex[q] = exps[((size_t)tile * splits + sp) * (W * RB) + blk];
+            in[q] = *(const u4 *)(src + (size_t)sp * kPerSplit);
         }
 #pragma unroll
-        for (int u = 0; u < SB; ++u)
-            if (sp0 + u < splits)
+        for (int q = 0; q < SB; ++q)
+            if (sp0 + q < splits) {
+                const uint32_t w[4] = {in[q].x, in[q].y, in[q].z, in[q].w};
 #pragma unroll
-                for (int cb = 0; cb < 4; ++cb) {
-                    const uint32_t w[4] = {in[u][cb].x, in[u][cb].y, in[u][cb].z, in[u][cb].w};
-#pragma unroll
-                    for (int q = 0; q < 8; ++q) {
-                        const float v =
-                            __builtin_amdgcn_ldexpf(half_bits_to_float((uint16_t)(w[q >> 1] >> (16 * (q & 1)))), ex[u]);
-                        t[cb][q] = sp0 + u == 0 ? v : t[cb][q] + v;
-                    }
+                for (int e = 0; e < 8; ++e) {
+                    const float v =
+                        __builtin_amdgcn_ldexpf(half_bits_to_float((uint16_t)(w[e >> 1] >> (16 * (e & 1)))), ex[q]);
+                    t[e] = sp0 + q == 0 ? v : t[e] + v;
                 }
+            }
     }
+    // element 8 vp + e of the 32x32 MFMA D block of lane l: row (e % 4) + 8 (e / 4) +
+    // 4 (l / 32) of the unit's 16, column 32 c + l % 32
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sums[(e & 3) + 8 * (e >> 2) + 4 * (lane >> 5)][32 * c + (lane & 31)] = t[e];
+    __syncthreads();
     const uint16_t *svp = (const uint16_t *)(records + (size_t)nb * kbs * group_bytes(bits) + 2048 * bits + 256);
-    gemm_rows_out<8>(t, lane, mt * BM + 32 * blk + 16 * vp, svp, rows, y, y_f16, y_stride, (size_t)nb * 128, res,
-                     res_stride);
+    const float sv0 = half_bits_to_float(svp[lane]), sv1 = half_bits_to_float(svp[lane + 64]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int rl = 4 * c + i, row = mt * BM + 32 * blk + 16 * vp + rl;
+        float a0 = sums[rl][lane], a1 = sums[rl][lane + 64];
+        h128_wave(a0, a1, lane);
+        a0 *= sv0;
+        a1 *= sv1;
+        if (row < rows) {
+            const size_t o = (size_t)row * y_stride + (size_t)nb * 128;
+            if (res) {  // y = res + layer, one rounding
+                const size_t ro = (size_t)row * res_stride + (size_t)nb * 128;
+                if (y_f16) {
+                    a0 += half_bits_to_float(((const uint16_t *)res)[ro + lane]);
+                    a1 += half_bits_to_float(((const uint16_t *)res)[ro + lane + 64]);
+                } else {
+                    a0 += ((const float *)res)[ro + lane];
+                    a1 += ((const float *)res)[ro + lane + 64];
+                }
+            }
+            if (y_f16) {
+                ((uint16_t *)y)[o + lane] = float_to_half_bits(a0);
+                ((uint16_t *)y)[o + lane + 64] = float_to_half_bits(a1);
+            } else {
+                ((float *)y)[o + lane] = a0;
+                ((float *)y)[o + lane + 64] = a1;
+            }
+        }
+    }
 }
 
 // Tile heights: 128 rows (4 waves, one 32-row block each), 256 (4 waves, two
@@ -550,14 +582,14 @@ static void launch_gemm_tiles(const uint8_t *rec, size_t k, uint16_t *xh, size_t
     static_assert(32 * RB * W == 128 || 32 * RB * W == 256 || 32 * RB * W == 512, "tile height");
     uint16_t *part = (uint16_t *)(ws + p.partials_off);
     int *exps = (int *)(ws + p.exps_off);
-    const int nwaves = p.mtiles * p.nbs * (p.bm / 16);  // reduction: one wave per 16 rows of a tile
+    const int nunits = p.mtiles * p.nbs * (p.bm / 16);  // reduction: one 4-wave workgroup per 16 rows of a tile
     const int kq = p.kbs / p.splits, kr = p.kbs % p.splits;
     gemm_kernel<K, CB, RB, W, NSG, XD><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, kq, kr, xh,
                                                                    k, part, exps, y, y_f16, y_stride, (int)rows, res,
                                                                    res_stride);
     if (p.splits > 1)
-        gemm_reduce_kernel<RB, W><<<dim3((unsigned)((nwaves + 3) / 4)), dim3(256), 0, stream>>>(
-            part, exps, p.splits, p.nbs, rec, K, p.kbs, y, y_f16, y_stride, (int)rows, nwaves, res, res_stride);
+        gemm_reduce_kernel<RB, W><<<dim3((unsigned)nunits), dim3(256), 0, stream>>>(
+            part, exps, p.splits, p.nbs, rec, K, p.kbs, y, y_f16, y_stride, (int)rows, nunits, res, res_stride);
 }
 
 template <int K, int CB>
