@@ -49,6 +49,7 @@ def parse():
     ap.add_argument("--only-gemv", action="store_true", help="headline GEMV only (for profiling)")
     ap.add_argument("--only-gemm", action="store_true", help="M=512 GEMM only (for profiling)")
     ap.add_argument("--only-c1", action="store_true", help="the k=2048 x n=6144 batch-1 GEMV only (for profiling)")
+    ap.add_argument("--only-rows", type=int, default=0, help="one C3 row count only (for profiling)")
     ap.add_argument("--no-extra", action="store_true", help="skip the C1/C2/C4/GET_ROWS lines")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only time a plain device copy of COPY_BYTES (scales the HBM byte counters)")
@@ -147,6 +148,16 @@ def main():
         stop.record(stream)
         torch.cuda.synchronize()
         return start.elapsed_time(stop) / steps, steps
+
+    if args.only_rows:
+        r = args.only_rows
+        xr = torch.from_numpy(synth.activations(1000 + r, r, K_IN)).to(dev)
+        ys[r] = torch.empty((r, N_OUT), dtype=torch.float16, device=dev)
+        ws[r] = amd.new_workspace(K_IN, N_OUT, r)
+        msr, n = timed(r, xr, args.steps, args.warmup)
+        print(json.dumps({"rows": r, "call_us": round(msr * 1e3, 2), "launches": n,
+                          "gbps": round(algo_bytes(K_IN, N_OUT, BITS, r) / (msr * 1e-3) / 1e9, 1)}), flush=True)
+        return
 
     if args.only_gemm:
         msg, n = timed(512, x512, max(36, args.steps // 2), max(18, args.warmup))

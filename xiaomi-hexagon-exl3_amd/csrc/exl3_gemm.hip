@@ -230,18 +230,25 @@ __device__ __forceinline__ void gemm_rows_out(float (&t)[4][NE], int lane, int r
     }
 }
 
-template <int K, int CB, int RB, int W, int NSG, int XD>
+// CH column halves: with CH = 2 the W waves are W / 2 row waves x 2 column
+// halves, each wave owning 32 RB rows x 64 columns (two accumulator blocks per
+// row block), so that a 128-row tile runs two waves per SIMD; such a tile always
+// has a k split (its epilogue writes partials only).
+template <int K, int CB, int RB, int W, int NSG, int XD, int CH>
 __global__ __launch_bounds__(W * 64) void gemm_kernel(
     const uint8_t *__restrict__ records, int kbs, int nbs, int mtiles, int splits, int kq, int kr,
     const uint16_t *__restrict__ xh16, size_t k, uint16_t *__restrict__ partials, int *__restrict__ exps, void *y,
     int y_f16, size_t y_stride, int rows, const void *res, size_t res_stride) {
-    constexpr int BM = 32 * RB * W;
+    constexpr int WR = W / CH;   // waves along the rows
+    constexpr int NCB = 4 / CH;  // 32-column accumulator blocks per row block of a wave
+    constexpr int BM = 32 * RB * WR;
     constexpr int H = 8 / W;  // trellis chunks a wave decodes per record
     constexpr size_t GB = (size_t)2048 * K + 512;
     __shared__ __attribute__((aligned(16))) uint16_t wlds[2][128 * 128];  // 64 KB
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rw = wave % WR, ch = wave / WR;  // row wave, column half
     const int lg = lane >> 4, li = lane & 15, j = li & 7;
     const int l32 = lane & 31, lh = lane >> 5;
     // Workgroups are dispatched to the 8 XCDs round-robin (blockIdx % 8) and each
@@ -293,32 +300,32 @@ __global__ __launch_bounds__(W * 64) void gemm_kernel(
         *(u4 *)(dst + gemm_w_offset(wn0[h] + 8 * (F >> 1), wc0[h] + (F & 1))) = fr;
     };
     // activations: A fragment (ks, rb) = the contiguous kilobyte of row block
-    // (BM mt + 32 (RB wave + rb)) / 32, record kb, k-step ks (gemm_xh_offset)
-    const uint16_t *xblk = xh16 + ((size_t)(mt * BM / 32 + RB * wave) * kbs * 8 * 64 + lane) * 8;
+    // (BM mt + 32 (RB rw + rb)) / 32, record kb, k-step ks (gemm_xh_offset)
+    const uint16_t *xblk = xh16 + ((size_t)(mt * BM / 32 + RB * rw) * kbs * 8 * 64 + lane) * 8;
     auto load_x_step = [&](int kb, int ks, h8 (&xs)[RB]) {
         const uint16_t *p = xblk + ((size_t)(kb < kb1 ? kb : kb1 - 1) * 8 + ks) * 512;
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) xs[rb] = *(const h8 *)(p + (size_t)rb * kbs * 8 * 512);
     };
-    // B fragment (ks, cb): column 32 cb + l32, k-chunk 2 ks + lh; the swizzle term
-    // depends on the lane and k-step only, so the four blocks sit at constant
-    // offsets from one address
-    auto read_b = [&](const uint16_t *wsrc, int ks, h8 (&b)[4]) {
-        const uint16_t *base = wsrc + l32 * 128 + (((2 * ks + lh) ^ li) << 3);
+    // B fragment (ks, cb): column 32 (NCB ch + cb) + l32, k-chunk 2 ks + lh; the
+    // swizzle term depends on the lane and k-step only, so the blocks sit at
+    // constant offsets from one address
+    auto read_b = [&](const uint16_t *wsrc, int ks, h8 (&b)[NCB]) {
+        const uint16_t *base = wsrc + l32 * 128 + (((2 * ks + lh) ^ li) << 3) + NCB * ch * 32 * 128;
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) b[cb] = *(const h8 *)(base + cb * 32 * 128);
+        for (int cb = 0; cb < NCB; ++cb) b[cb] = *(const h8 *)(base + cb * 32 * 128);
     };
 
-    f16v acc[RB][4];
+    f16v acc[RB][NCB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb)
+        for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[rb][cb][e] = 0.f;
-    auto mma_step = [&](const h8 (&xs)[RB], const h8 (&b)[4]) {
+    auto mma_step = [&](const h8 (&xs)[RB], const h8 (&b)[NCB]) {
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb)
+        for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb)
                 acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xs[rb], b[cb], acc[rb][cb], 0, 0, 0);
@@ -344,13 +351,13 @@ __global__ __launch_bounds__(W * 64) void gemm_kernel(
         decode_piece(std::integral_constant<int, 7>{}, wbuf[0], xb, wlds[0]);
     }
     __syncthreads();
-    h8 bc[4], bn[4];
+    h8 bc[NCB], bn[NCB];
     read_b(wlds[0], 0, bc);
 
     // one k-step: B of ks + 1 requested, MFMAs of ks, a decode piece, then the
     // activations of ks for the next record
     auto kstep = [&](auto kc, int kb, const uint16_t *wcur, uint16_t *wnext, const uint32_t (&wnextw)[H][K],
-                     h8 (&bcur)[4], h8 (&bnxt)[4]) {
+                     h8 (&bcur)[NCB], h8 (&bnxt)[NCB]) {
         constexpr int KS = decltype(kc)::value;
         if constexpr (KS < 7) read_b(wcur, KS + 1, bnxt);
         mma_step(xa[KS % XD], bcur);
@@ -405,55 +412,56 @@ __global__ __launch_bounds__(W * 64) void gemm_kernel(
         }
     }
 
-    // epilogue.  acc[rb][cb][e]: row 32 RB wave + 32 rb + (e % 4) + 8 (e / 4) + 4 lh,
-    // column 32 cb + l32
+    // epilogue.  acc[rb][cb][e]: row 32 RB rw + 32 rb + (e % 4) + 8 (e / 4) + 4 lh,
+    // column 32 (NCB ch + cb) + l32
     if (splits > 1) {
-        // fp16 partials in accumulator layout [tile][split][wave][rb][cb][vp][lane]
-        // x 16 bytes: elements 8 vp .. 8 vp + 7 of acc[rb][cb] (rows of v = 2 vp,
-        // 2 vp + 1), summed in fp32 by gemm_reduce_kernel.  Each (wave, rb) block
-        // is stored scaled by 2^-e, e = exps[(tile, split, wave, rb)] chosen so that
-        // its largest magnitude is below 2^14: fp16's relative precision for every
-        // value, and no overflow however large the activations.  fp16 keeps the
-        // layer within its tolerance (rel-L2 2.9e-4 against 2.1e-4 for fp32
-        // partials with fp16 output, at k = 14336) for half the bytes.
-        constexpr size_t kPerSplit = (size_t)W * RB * 4 * 2 * 64 * 8;  // halves
-        uint16_t *dst = partials + ((size_t)tile * splits + s) * kPerSplit + (size_t)wave * RB * 8 * 512 + lane * 8;
+        // fp16 partials in accumulator layout [tile][split][rw][rb][column block][vp]
+        // [lane] x 16 bytes: elements 8 vp .. 8 vp + 7 of a 32x32 block (rows of
+        // v = 2 vp, 2 vp + 1), summed in fp32 by gemm_reduce_kernel.  Each 32x32
+        // block is stored scaled by 2^-e, e = exps[(tile, split, rw, rb, block)]
+        // chosen so that its largest magnitude is below 2^14: fp16's relative
+        // precision for every value, and no overflow however large the activations.
+        // fp16 keeps the layer within its tolerance (rel-L2 2.9e-4 against 2.1e-4
+        // for fp32 partials with fp16 output, at k = 14336) for half the bytes.
+        constexpr size_t kPerSplit = (size_t)WR * RB * 4 * 2 * 64 * 8;  // halves
+        uint16_t *dst = partials + ((size_t)tile * splits + s) * kPerSplit + (size_t)rw * RB * 8 * 512 + lane * 8;
         auto pk = [](float a, float b, int e) {
             return (uint32_t)float_to_half_bits(__builtin_amdgcn_ldexpf(a, -e)) |
                    ((uint32_t)float_to_half_bits(__builtin_amdgcn_ldexpf(b, -e)) << 16);
         };
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-            float m = 0.f;
+        for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-            for (int cb = 0; cb < 4; ++cb)
+            for (int cb = 0; cb < NCB; ++cb) {
+                const int cg = NCB * ch + cb;  // column block in the tile
+                float m = 0.f;
 #pragma unroll
                 for (int e = 0; e < 16; ++e) m = fmaxf(m, fabsf(acc[rb][cb][e]));
-            m = wave_max(m);
-            const int ex = __builtin_amdgcn_frexp_expf(m) - 14;  // m < 2^(ex + 14); 0 (and Inf, NaN): -14
-            if (lane == 0) exps[((size_t)tile * splits + s) * (W * RB) + wave * RB + rb] = ex;
-#pragma unroll
-            for (int cb = 0; cb < 4; ++cb)
+                m = wave_max(m);
+                const int ex = __builtin_amdgcn_frexp_expf(m) - 14;  // m < 2^(ex + 14); 0 (and Inf, NaN): -14
+                if (lane == 0) exps[(((size_t)tile * splits + s) * (WR * RB) + rw * RB + rb) * 4 + cg] = ex;
 #pragma unroll
                 for (int vp = 0; vp < 2; ++vp) {
                     const f16v &a = acc[rb][cb];
                     const u4 d = {pk(a[8 * vp], a[8 * vp + 1], ex), pk(a[8 * vp + 2], a[8 * vp + 3], ex),
                                   pk(a[8 * vp + 4], a[8 * vp + 5], ex), pk(a[8 * vp + 6], a[8 * vp + 7], ex)};
-                    __builtin_nontemporal_store(d, (u4 *)(dst + ((rb * 4 + cb) * 2 + vp) * 512));
+                    __builtin_nontemporal_store(d, (u4 *)(dst + ((rb * 4 + cg) * 2 + vp) * 512));
                 }
-        }
+            }
         return;
     }
-    const uint16_t *svp = (const uint16_t *)(colgroup + 2048 * K + 256);  // record (nb, 0)
+    if constexpr (CH == 1) {  // whole rows in one wave: H128 and sv here
+        const uint16_t *svp = (const uint16_t *)(colgroup + 2048 * K + 256);  // record (nb, 0)
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-        float t[4][16];
+        for (int rb = 0; rb < RB; ++rb) {
+            float t[4][16];
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb)
+            for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) t[cb][e] = acc[rb][cb][e];
-        gemm_rows_out<16>(t, lane, mt * BM + 32 * RB * wave + 32 * rb, svp, rows, y, y_f16, y_stride, (size_t)nb * 128,
-                          res, res_stride);
+                for (int e = 0; e < 16; ++e) t[cb][e] = acc[rb][cb][e];
+            gemm_rows_out<16>(t, lane, mt * BM + 32 * RB * rw + 32 * rb, svp, rows, y, y_f16, y_stride,
+                              (size_t)nb * 128, res, res_stride);
+        }
     }
 }
 
@@ -490,7 +498,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const uint16_t *__rest
 #pragma unroll
         for (int q = 0; q < SB; ++q) {
             const int sp = sp0 + q < splits ? sp0 + q : splits - 1;
-            ex[q] = exps[((size_t)tile * splits + sp) * (W * RB) + blk];
+            ex[q] = exps[(((size_t)tile * splits + sp) * (W * RB) + blk) * 4 + c];
             in[q] = *(const u4 *)(src + (size_t)sp * kPerSplit);
         }
 #pragma unroll
@@ -567,28 +575,29 @@ GemmPlan gemm_plan(size_t k, size_t n, size_t rows) {
     p.partials_off = off;
     if (s > 1) off += (size_t)tiles * s * p.bm * 128 * 2;  // fp16 partials
     p.exps_off = off;
-    if (s > 1) off += ((size_t)tiles * s * (p.bm / 32) * 4 + 255) & ~(size_t)255;  // one exponent per 32-row block
+    if (s > 1) off += ((size_t)tiles * s * (p.bm / 32) * 4 * 4 + 255) & ~(size_t)255;  // one per 32x32 block
     p.bytes = (off + 255) & ~(size_t)255;
     return p;
 }
 
 // one tile class: kernel <RB, W> (NSG scheduling groups per k-step, XD activation
 // k-steps in flight) and its reduction
-template <int K, int CB, int RB, int W, int NSG, int XD>
+template <int K, int CB, int RB, int W, int NSG, int XD, int CH>
 static void launch_gemm_tiles(const uint8_t *rec, size_t k, uint16_t *xh, size_t rows, void *y, int y_f16,
                               size_t y_stride, uint8_t *ws, const GemmPlan &p, hipStream_t stream, const void *res,
                               size_t res_stride) {
+    constexpr int WR = W / CH;  // the reduction sees the row waves
+    static_assert(32 * RB * WR == 128 || 32 * RB * WR == 256 || 32 * RB * WR == 512, "tile height");
     const dim3 grid((unsigned)(p.mtiles * p.nbs * p.splits)), block(W * 64);
-    static_assert(32 * RB * W == 128 || 32 * RB * W == 256 || 32 * RB * W == 512, "tile height");
     uint16_t *part = (uint16_t *)(ws + p.partials_off);
     int *exps = (int *)(ws + p.exps_off);
     const int nunits = p.mtiles * p.nbs * (p.bm / 16);  // reduction: one 4-wave workgroup per 16 rows of a tile
     const int kq = p.kbs / p.splits, kr = p.kbs % p.splits;
-    gemm_kernel<K, CB, RB, W, NSG, XD><<<grid, block, 0, stream>>>(rec, p.kbs, p.nbs, p.mtiles, p.splits, kq, kr, xh,
-                                                                   k, part, exps, y, y_f16, y_stride, (int)rows, res,
-                                                                   res_stride);
+    gemm_kernel<K, CB, RB, W, NSG, XD, CH><<<grid, block, 0, stream>>>(
+        rec, p.kbs, p.nbs, p.mtiles, p.splits, kq, kr, xh, k, part, exps, y, y_f16, y_stride, (int)rows, res,
+        res_stride);
     if (p.splits > 1)
-        gemm_reduce_kernel<RB, W><<<dim3((unsigned)nunits), dim3(256), 0, stream>>>(
+        gemm_reduce_kernel<RB, WR><<<dim3((unsigned)nunits), dim3(256), 0, stream>>>(
             part, exps, p.splits, p.nbs, rec, K, p.kbs, y, y_f16, y_stride, (int)rows, nunits, res, res_stride);
 }
 
@@ -596,12 +605,14 @@ template <int K, int CB>
 static void launch_gemm_kc(const uint8_t *rec, size_t k, uint16_t *xh, size_t rows, void *y, int y_f16,
                            size_t y_stride, uint8_t *ws, const GemmPlan &p, hipStream_t stream, const void *res,
                            size_t res_stride) {
-    if (p.bm == 128)
-        launch_gemm_tiles<K, CB, 1, 4, 8, 8>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream, res, res_stride);
+    if (p.bm == 128 && p.splits > 1)  // 8 waves: 4 row waves x 2 column halves, two waves per SIMD
+        launch_gemm_tiles<K, CB, 1, 8, 0, 8, 2>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream, res, res_stride);
+    else if (p.bm == 128)
+        launch_gemm_tiles<K, CB, 1, 4, 8, 8, 1>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream, res, res_stride);
     else if (p.bm == 256)
-        launch_gemm_tiles<K, CB, 2, 4, 8, 8>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream, res, res_stride);
+        launch_gemm_tiles<K, CB, 2, 4, 8, 8, 1>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream, res, res_stride);
     else  // 8 waves: no scheduling groups, four activation k-steps in flight (measured best at M = 512)
-        launch_gemm_tiles<K, CB, 2, 8, 0, 4>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream, res, res_stride);
+        launch_gemm_tiles<K, CB, 2, 8, 0, 4, 1>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream, res, res_stride);
 }
 
 template <int K>
