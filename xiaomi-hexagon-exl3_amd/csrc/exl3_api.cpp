@@ -147,12 +147,12 @@ size_t exl3_hip_mul_mat_workspace_bytes(size_t k, size_t n, size_t rows) {
         const exl3k::GemvPlan p = exl3k::gemv_plan(k, n, r);
         need = std::max(need, p.fits ? p.bytes : exl3k::gemm_plan(k, n, r).bytes);
     }
-    // GEMM plans: one tile height per row range, the largest row count of each
-    // m-tile count within it
+    // GEMM plans: the largest row count of each (tile height, m-tile count) run;
+    // r_hi >= r, so every pass moves on
     for (size_t r = exl3k::kGemvMaxRows + 1; r <= rows;) {
-        const size_t bm = (size_t)exl3k::gemm_tile_rows(r);
-        const size_t class_end = bm < 512 ? bm : rows;
-        const size_t r_hi = std::min(rows, std::min(class_end, (r + bm - 1) / bm * bm));
+        const int bm = exl3k::gemm_tile_rows(r);
+        size_t r_hi = std::min(rows, (r + bm - 1) / bm * bm);
+        while (exl3k::gemm_tile_rows(r_hi) != bm) --r_hi;
         need = std::max(need, exl3k::gemm_plan(k, n, r_hi).bytes);
         r = r_hi + 1;
     }
