@@ -115,15 +115,14 @@ int exl3_hip_supports_op(exl3_op op, const exl3_tensor_info *dst, const exl3_ten
                          const exl3_tensor_info *src1);
 
 /* Device workspace bytes exl3_hip_mul_mat needs for (k, n) at any row count
- * 1..rows.  The workspace starts with the split-K sync words and hand-off words
- * (max(n/128, 512) x 8 bytes rounded up to 256, then 16 MiB), which every call
- * leaves zero, followed by per-call staging: zero-fill it once before its first
- * use (exl3_hip_workspace_init).  One workspace serves any sequence of calls
- * whose n agree, or all stay <= 65536, when it holds at least
- * exl3_hip_mul_mat_workspace_bytes(k, n, rows) of every one of them; calls that
- * share one must not run concurrently (order them on one stream).  A call of at
- * most exl3_hip_gemv_max_rows() rows whose split-K partials would not fit the
- * 16 MiB runs the GEMM path (k * n above about 134 M weights at 32 rows). */
+ * 1..rows.  The workspace starts with the 16 MiB of split-K hand-off words,
+ * which every call leaves zero, followed by per-call staging: zero-fill it once
+ * before its first use (exl3_hip_workspace_init).  One workspace serves any
+ * sequence of calls when it holds at least exl3_hip_mul_mat_workspace_bytes(k,
+ * n, rows) of every one of them; calls that share one must not run concurrently
+ * (order them on one stream).  A call of at most exl3_hip_gemv_max_rows() rows
+ * whose split-K partials would not fit the 16 MiB runs the GEMM path (k * n
+ * above about 134 M weights at 32 rows). */
 size_t exl3_hip_mul_mat_workspace_bytes(size_t k, size_t n, size_t rows);
 exl3_status exl3_hip_workspace_init(void *workspace, size_t workspace_bytes, hipStream_t stream);
 
@@ -160,8 +159,8 @@ exl3_status exl3_hip_mul_mat(const void *records, unsigned bits, unsigned codebo
  * HIP-graph capture, serving loops or harnesses that forbid hipMalloc).  The
  * workspace is a 64 MiB device array inside the library, one per GPU, held
  * until the process ends; a call whose exl3_hip_mul_mat_workspace_bytes(k, n,
- * rows) exceeds it returns EXL3_WORKSPACE_TOO_SMALL, and n above 65536 returns
- * EXL3_INVAL_PARAMS, before anything is enqueued.  Every call on a GPU shares
+ * rows) exceeds it returns EXL3_WORKSPACE_TOO_SMALL before anything is
+ * enqueued.  Every call on a GPU shares
  * that GPU's array: calls that overlap on one GPU (different streams, or
  * threads without ordering) race and give wrong results; order them on one
  * stream.  Results equal exl3_hip_mul_mat's bit for bit. */

@@ -284,12 +284,12 @@ def test_concurrent_streams(amd):
 
 
 def test_one_workspace_serves_mixed_widths(amd):
-    """One caller workspace shared by layers of different n (all <= 65536) and
-    both kernels: a GEMM call at n=2048 (its activation staging sits behind the
-    sync words and the split-K exchange), then GEMV calls at n=14336 (more column
-    groups, so more sync words) and a gate/up group (n = 2 x 6144).  Those regions
-    do not depend on n, so no call writes over another's: every result equals
-    the one from a fresh workspace, over two rounds of the sequence."""
+    """One caller workspace shared by layers of different n and both kernels: a
+    GEMM call at n=2048 (its activation staging sits behind the split-K
+    exchange), then GEMV calls at n=14336 (more column groups) and a gate/up
+    group (n = 2 x 6144).  The exchange does not depend on n, so no call writes
+    over another's: every result equals the one from a fresh workspace, over two
+    rounds of the sequence."""
     import torch
     cases = {  # name: (k, [n...], rows, bits)
         "gemm_n2048": (4096, [2048], 64, 4),
@@ -356,14 +356,14 @@ def test_internal_workspace_under_capture(amd):
         assert torch.equal(y, eager)
 
 
-# bytes every workspace of n <= 65536 starts with: 512 64-bit arrival counters,
-# then the 16 MiB of split-K hand-off words (both zero between calls)
-SHARED_PREFIX = 512 * 8 + (16 << 20)
+# bytes every workspace starts with: the 16 MiB of split-K hand-off words (zero
+# between calls)
+SHARED_PREFIX = 16 << 20
 
 
 def test_exchange_left_empty(amd):
-    """The split-K hand-off leaves the workspace's sync words and exchange zero
-    after every GEMV call (its last workgroups empty what they read), and GEMM
+    """The split-K hand-off leaves the workspace's exchange zero after every GEMV
+    call (the workgroups that sum the splits empty what they read), and GEMM
     calls never write there: a caller workspace used for GEMV calls of 1..32
     rows, a group call and GEMM calls is zero over its first SHARED_PREFIX bytes
     after each call, and every result equals the one from a fresh workspace."""
@@ -380,7 +380,7 @@ def test_exchange_left_empty(amd):
         torch.cuda.synchronize()
         assert torch.equal(y, fresh), f"call {i} rows={rows}"
         nz = int(torch.count_nonzero(ws[:SHARED_PREFIX]))
-        assert nz == 0, f"call {i} rows={rows}: {nz} nonzero bytes left in the sync words / exchange"
+        assert nz == 0, f"call {i} rows={rows}: {nz} nonzero bytes left in the exchange"
     mats = [(dev(make_layer(1400 + j, 2048, 6144, 4)), 6144) for j in range(2)]
     wsg = amd.new_workspace(2048, 2 * 6144, 8)
     for rows in (3, 8):

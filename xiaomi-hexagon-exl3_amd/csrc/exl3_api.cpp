@@ -10,7 +10,6 @@
 #include <map>
 #include <mutex>
 #include <algorithm>
-#include <tuple>
 #include <utility>
 #include <vector>
 
@@ -32,10 +31,8 @@ bool valid_matrix(size_t k, size_t n, size_t multiple) {
     return k && n && k % multiple == 0 && n % multiple == 0 && k <= kMaxDim && n <= kMaxDim;
 }
 
-// Internal workspaces, one per (device, stream, counter-region size), grown on
-// demand, zero-filled when created and kept until process exit.  Calls that
-// share one have the same counter layout (exl3k::counter_region_bytes).  A
-// workspace that is outgrown is retired, never freed: a call on another thread
+// Internal workspaces, one per (device, stream), grown on demand, zero-filled
+// when created and kept until process exit.  A workspace that is outgrown is retired, never freed: a call on another thread
 // may still be enqueuing kernels that use it.  Growth allocates, so it is
 // refused while the stream is being captured into a HIP graph: a caller that
 // captures passes its own workspace, or makes one uncaptured call of the
@@ -45,14 +42,14 @@ struct InternalWs {
     size_t bytes = 0;
 };
 std::mutex g_ws_mutex;
-std::map<std::tuple<int, hipStream_t, size_t>, InternalWs> g_ws;
+std::map<std::pair<int, hipStream_t>, InternalWs> g_ws;
 std::vector<void *> g_ws_retired;
 
-exl3_status internal_workspace(size_t need, size_t n, hipStream_t stream, void **out) {
+exl3_status internal_workspace(size_t need, hipStream_t stream, void **out) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return EXL3_HIP_ERROR;
     std::lock_guard<std::mutex> lock(g_ws_mutex);
-    InternalWs &ws = g_ws[std::make_tuple(dev, stream, exl3k::counter_region_bytes(n))];
+    InternalWs &ws = g_ws[std::make_pair(dev, stream)];
     if (ws.bytes < need) {
         hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
         if (hipStreamIsCapturing(stream, &capture) != hipSuccess) return EXL3_HIP_ERROR;
@@ -178,7 +175,7 @@ static exl3_status mul_mat_impl(const void *records, unsigned bits, unsigned cod
         if (!aligned(workspace, 256)) return EXL3_INVAL_PARAMS;
         if (workspace_bytes < need) return EXL3_WORKSPACE_TOO_SMALL;
     } else {
-        const exl3_status st = internal_workspace(need, n, stream, &workspace);
+        const exl3_status st = internal_workspace(need, stream, &workspace);
         if (st != EXL3_OK) return st;
     }
     const int xf = xt == EXL3_F16, yf = yt == EXL3_F16;
@@ -243,7 +240,7 @@ exl3_status exl3_hip_mul_mat_group(const exl3_matrix_desc *mats, size_t count, u
         if (!aligned(workspace, 256)) return EXL3_INVAL_PARAMS;
         if (workspace_bytes < need) return EXL3_WORKSPACE_TOO_SMALL;
     } else {
-        const exl3_status st = internal_workspace(need, n_total, stream, &workspace);
+        const exl3_status st = internal_workspace(need, stream, &workspace);
         if (st != EXL3_OK) return st;
     }
     exl3k::GemvTargets tg{};
@@ -391,7 +388,7 @@ exl3_status exl3_hip_iface_matmul(unsigned bits, unsigned codebook, size_t k, si
         if (!aligned(workspace, 256)) return EXL3_INVAL_PARAMS;
         if (workspace_bytes < need) return EXL3_WORKSPACE_TOO_SMALL;
     } else {
-        const exl3_status st = internal_workspace(need, n, stream, &workspace);
+        const exl3_status st = internal_workspace(need, stream, &workspace);
         if (st != EXL3_OK) return st;
     }
     const size_t roff = iface_records_offset(k, n, batch);

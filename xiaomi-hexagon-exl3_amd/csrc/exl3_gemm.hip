@@ -568,8 +568,7 @@ GemmPlan gemm_plan(size_t k, size_t n, size_t rows) {
     const int smax = p.kbs / 4 > 0 ? p.kbs / 4 : 1;
     s = s < 1 ? 1 : (s > smax ? smax : s);
     p.splits = s;
-    p.counters_off = 0;  // the GEMM leaves the sync words and the GEMV exchange alone
-    size_t off = shared_prefix_bytes(n);
+    size_t off = kSharedPrefixBytes;  // the GEMM leaves the GEMV exchange alone
     p.xh_off = off;
     off += ((size_t)p.mtiles * p.bm * k * 2 + 255) & ~(size_t)255;
     p.partials_off = off;

@@ -63,8 +63,8 @@ constexpr size_t kGemvFragLds16 = 65536;  // the same for rows 9..16 (two workgr
 template <int K, int CB, int MODE>
 __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void gemv_kernel(
     GemvTargets tg, int kbs, int splits, int kq, int kr, const void *__restrict__ x, int x_f16, size_t x_stride,
-    int rows, const uint8_t *__restrict__ dummy, uint32_t *__restrict__ partials, uint64_t *__restrict__ sync,
-    int y_f16, const uint8_t *__restrict__ xpre) {
+    int rows, const uint8_t *__restrict__ dummy, uint32_t *__restrict__ partials, int y_f16,
+    const uint8_t *__restrict__ xpre) {
     constexpr bool TWO = MODE >= 1, HILO = MODE <= 1;
     constexpr int W = kGemvWaves;
     constexpr int P = W / 4;  // waves per column pair
@@ -74,7 +74,6 @@ __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu
     // K <= 2 keeps them within 128 VGPRs (two workgroups per CU)
     constexpr int D = TWO && K <= 2 ? 8 : GemvStream<K>::DEPTH;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    __shared__ unsigned claim_lds;  // arrivals before this workgroup's (split-K)
     uint8_t *frag = smem;
     // B fragments of one (kb, r4, half): [kg][hl][row] x 16 bytes (MODE 2: [kg][row])
     const int blk_bytes = (HILO ? 128 : 64) * rows;
@@ -407,36 +406,39 @@ __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu
             ((float *)y)[o + lane + 64] = a1;
         }
     };
+    float *own = red + P * nval;  // the workgroup partial, for the output rows
     if (splits > 1) {
-        // every workgroup hands its partial over in the exchange, waits for those
-        // stores to complete (so the last workgroup finds them in place and its
-        // re-read below stays a formality) and claims its arrival
-        uint32_t *mine = partials + ((size_t)nb * splits + s) * (size_t)nval;
+        uint32_t *all = partials + (size_t)nb * splits * (size_t)nval;
+        if (s != splits - 1) {  // hand the partial over and end
+            uint32_t *mine = all + (size_t)s * nval;
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int t = tid + i * NT;
+                if (t < nval) store_exchange(mine + t, psum[i]);
+            }
+            return;
+        }
+        // the last split: wave r sums row r's elements lane and lane + 64 over
+        // the splits in split order, its own partial (from LDS) last, a batch of
+        // splits' loads in flight together, straight into the registers of the
+        // output transform.  A word still empty is read again (with the rest of
+        // its batch) until it is full.
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int t = tid + i * NT;
-            if (t < nval) store_exchange(mine + t, psum[i]);
+            if (t < nval) own[t] = psum[i];
         }
-        wait_stores();
         __syncthreads();
-        if (tid == 0) claim_lds = claim_arrival(sync + nb);
-        __syncthreads();
-        if (claim_lds != (unsigned)splits - 1) return;
-        // the last workgroup: wave r sums row r's elements lane and lane + 64 over
-        // the splits in split order (so the result does not depend on which
-        // workgroup arrived last), a batch of splits' loads in flight together,
-        // straight into the registers of the output transform.  A word still
-        // empty is read again (with the rest of its batch) until it is full.
-        uint32_t *all = partials + (size_t)nb * splits * (size_t)nval;
+        const int nsp = splits - 1;  // splits in the exchange
         for (int rr = wave; rr < rows; rr += W) {
             constexpr int B = 16;
             float a0 = 0.f, a1 = 0.f;
-            for (int base = 0; base < splits; base += B) {
+            for (int base = 0; base < nsp; base += B) {
                 uint32_t v0[B], v1[B];
                 auto load_batch = [&](int bs, int rw) {
 #pragma unroll
                     for (int jb = 0; jb < B; ++jb) {
-                        const int sp = bs + jb < splits ? bs + jb : splits - 1;  // repeats are not used
+                        const int sp = bs + jb < nsp ? bs + jb : nsp - 1;  // repeats are not used
                         const uint32_t *q = all + (size_t)sp * nval + rw * 128 + lane;
                         v0[jb] = load_exchange(q);
                         v1[jb] = load_exchange(q + 64);
@@ -447,7 +449,7 @@ __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu
                     int z = 0;
 #pragma unroll
                     for (int jb = 0; jb < B; ++jb)
-                        if (base + jb < splits) z |= (v0[jb] == 0u) | (v1[jb] == 0u);
+                        if (base + jb < nsp) z |= (v0[jb] == 0u) | (v1[jb] == 0u);
                     return z != 0;
                 };
                 for (int pass = 0; __builtin_amdgcn_ballot_w64(any_empty()) && pass < kExchangeSpinLimit; ++pass) {
@@ -460,29 +462,26 @@ __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu
                 }
 #pragma unroll
                 for (int jb = 0; jb < B; ++jb)
-                    if (base + jb < splits) {  // a word that never filled: a loud result, not a hang
+                    if (base + jb < nsp) {  // a word that never filled: a loud result, not a hang
                         a0 += v0[jb] ? exchange_value(v0[jb]) : __builtin_nanf("");
                         a1 += v1[jb] ? exchange_value(v1[jb]) : __builtin_nanf("");
                     }
             }
-            finish_row(rr, a0, a1);
+            finish_row(rr, a0 + own[rr * 128 + lane], a1 + own[rr * 128 + lane + 64]);
         }
-        // every word has been read: empty them and the arrival count for the next call
+        // every word has been read: empty them for the next call
         __syncthreads();
-        for (int t = tid; t < splits * nval; t += NT) clear_exchange(all + t);
-        if (tid == 0) clear_sync(sync + nb);
+        for (int t = tid; t < nsp * nval; t += NT) clear_exchange(all + t);
         return;
     }
     // 6. (one workgroup per column group) output H128 per row from the LDS sums
-    float *ybuf = red + P * nval;
-    __syncthreads();
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const int t = tid + i * NT;
-        if (t < nval) ybuf[t] = psum[i];
+        if (t < nval) own[t] = psum[i];
     }
     __syncthreads();
-    for (int rr = wave; rr < rows; rr += W) finish_row(rr, ybuf[rr * 128 + lane], ybuf[rr * 128 + lane + 64]);
+    for (int rr = wave; rr < rows; rr += W) finish_row(rr, own[rr * 128 + lane], own[rr * 128 + lane + 64]);
 }
 
 // Activations of the 17..32-row GEMV (MODE 2): fp16(H128(x[r] su)), su from record
@@ -555,11 +554,10 @@ GemvPlan gemv_plan(size_t k, size_t n, size_t rows) {
     }
     p.splits = s;
     p.nkw = (p.kbs + s - 1) / s;
-    p.counters_off = 0;
-    p.partials_off = exchange_offset(n);
+    p.partials_off = 0;  // the exchange
     p.exchange_bytes = s > 1 ? (size_t)p.nbs * s * rows * 128 * 4 : 0;  // one 32-bit word per partial value
     p.fits = p.exchange_bytes <= kGemvExchangeBytes;
-    size_t off = shared_prefix_bytes(n);
+    size_t off = kSharedPrefixBytes;
     p.dummy_off = off;  // target of the stream's issues past a wave's last group (loaded, never used)
     off += kGemvDummyBytes;
     p.xpre_off = off;  // rows > 16: prepared activations of up to kGemvMaxTargets matrices
@@ -576,24 +574,24 @@ template <int K, int CB>
 static hipError_t launch_gemv_kc(const GemvTargets &tg, const void *x, int x_f16, size_t rows, size_t x_stride,
                                  int y_f16, uint8_t *ws, const GemvPlan &p, hipStream_t stream) {
     const size_t lds = gemv_lds_bytes(p.nkw, rows);
-    // x fastest: workgroup (nb, s) is dispatched as nb + s nbs, as a 1-D grid would be
+    // x fastest: workgroup (nb, s) is dispatched as nb + s nbs, as a 1-D grid would
+    // be, so the last split's workgroups, which wait for the others, come last
     const dim3 grid((unsigned)p.nbs, (unsigned)p.splits), block(kGemvWaves * 64);
     const int kq = p.kbs / p.splits, kr = p.kbs % p.splits;
     uint32_t *part = (uint32_t *)(ws + p.partials_off);
-    uint64_t *sync = (uint64_t *)(ws + p.counters_off);
     if (rows > 16) {
         uint16_t *xp = (uint16_t *)(ws + p.xpre_off);
         gemv_xprep_kernel<<<dim3((unsigned)((rows + 3) / 4), (unsigned)p.kbs, (unsigned)tg.count), dim3(256), 0,
                             stream>>>(tg, K, x, x_f16, x_stride, (int)rows, p.kbs, xp);
         gemv_kernel<K, CB, 2><<<grid, block, lds, stream>>>(tg, p.kbs, p.splits, kq, kr, x, x_f16, x_stride,
-                                                            (int)rows, ws + p.dummy_off, part, sync, y_f16,
+                                                            (int)rows, ws + p.dummy_off, part, y_f16,
                                                             (const uint8_t *)xp);
     } else if (rows > 8) {
         gemv_kernel<K, CB, 1><<<grid, block, lds, stream>>>(tg, p.kbs, p.splits, kq, kr, x, x_f16, x_stride,
-                                                            (int)rows, ws + p.dummy_off, part, sync, y_f16, nullptr);
+                                                            (int)rows, ws + p.dummy_off, part, y_f16, nullptr);
     } else {
         gemv_kernel<K, CB, 0><<<grid, block, lds, stream>>>(tg, p.kbs, p.splits, kq, kr, x, x_f16, x_stride,
-                                                            (int)rows, ws + p.dummy_off, part, sync, y_f16, nullptr);
+                                                            (int)rows, ws + p.dummy_off, part, y_f16, nullptr);
     }
     return hipGetLastError();
 }

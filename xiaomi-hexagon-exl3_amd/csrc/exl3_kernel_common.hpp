@@ -31,29 +31,24 @@ __device__ __forceinline__ float mul_rn_f32(float a, float b) {
 // Split-K hand-off through L2, without cache maintenance.  The partial sums of
 // a column group's k-splits cross XCDs (each XCD has its own L2), through the
 // workspace's exchange: 32-bit words, zero ("empty") between calls.  Every
-// workgroup stores its partial there as relaxed agent-scope atomics (sc1:
-// coherent at device scope), each value complemented and never zero
-// (exchange_bits), then claims its arrival with a relaxed agent-scope fetch_add
-// on the column group's sync word.  The one that sees the last arrival count
-// sums the partials, reading again (in batches, boundedly) any word still
-// empty, then zeroes every word and the sync word, so the next call finds the
-// same state.  Within a call each word is zero or holds the value its one
-// writer stored, and 32-bit words are single-copy atomic: a nonzero word is
-// this call's value, whatever order the other words arrive in.  That is why no
-// release/acquire pair is needed; an agent-scope fence writes back or
-// invalidates the whole L2 on gfx950 (measured 14.6 -> 53.8 us per GEMV call at
-// k = 14336, n = 4096).  Writers wait for their stores to complete before they
-// claim, so in practice the last workgroup never reads a word twice.
+// workgroup but the column group's last split stores its partial there as
+// relaxed agent-scope atomics (sc1: coherent at device scope), each value
+// complemented and never zero (exchange_bits), and ends.  The last split's
+// workgroup (the highest workgroup index of its column group) keeps its own
+// partial in LDS, reads the other splits' words, reading again (in batches,
+// boundedly) any word still empty, sums all splits in split order, then zeroes
+// every word it read, so the next call finds the same state.  Within a call
+// each word is zero or holds the value its one writer stored, and 32-bit words
+// are single-copy atomic: a nonzero word is this call's value, whatever order
+// the words arrive in.  That is why no release/acquire pair is needed; an
+// agent-scope fence writes back or invalidates the whole L2 on gfx950 (measured
+// 14.6 -> 53.8 us per GEMV call at k = 14336, n = 4096).  Only the summing
+// workgroups wait, and only for workgroups that wait for nothing.  The split is
+// the grid's slowest dimension, so the summing workgroups are the grid's last:
+// on every XCD the others are dispatched before any of them and never need a
+// slot that a waiting workgroup holds, and every wait ends.
 constexpr int kExchangeSpinLimit = 1 << 20;
 
-__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-__device__ __forceinline__ unsigned claim_arrival(uint64_t *sync) {  // arrivals before this one
-    return (unsigned)__hip_atomic_fetch_add((unsigned long long *)sync, 1ull, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void clear_sync(uint64_t *sync) {
-    __hip_atomic_store((unsigned long long *)sync, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 // binary32 bits complemented; the one value whose complement is zero (the NaN
 // 0xffffffff) is stored as 1, which reads back as the NaN 0xfffffffe
 __device__ __forceinline__ uint32_t exchange_bits(float v) {

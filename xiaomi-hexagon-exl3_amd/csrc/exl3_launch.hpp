@@ -14,27 +14,19 @@ namespace exl3k {
 constexpr int kGemvMaxRows = 32;
 constexpr int kGemvWaves = 8;     // waves per GEMV workgroup (a multiple of 4)
 
-// Every plan starts with the same two regions, which only the GEMV's split-K
-// hand-off touches:
-//   1. sync words: one 64-bit arrival counter per column group, at least
-//      kCounterFloor of them whatever n is (counter_region_bytes);
-//   2. the exchange: kGemvExchangeBytes of 64-bit words carrying split partials.
-// Both are zero before a workspace's first use and every GEMV call leaves them
-// zero again (its last workgroups clear what they consumed), and no other
-// kernel writes them.  One workspace therefore serves calls of any row count
-// (and any k) in turn, and calls whose n differ but stay within 128 *
-// kCounterFloor = 65536 columns put every region at the same offset.  A GEMV
-// whose partials would not fit the exchange runs as a GEMM instead.  The GEMM
-// splits k only while it has fewer than kGemmSplitTiles output tiles; a second
-// kernel sums its split partials.
+// Every plan starts with the same region, which only the GEMV's split-K hand-off
+// touches: the exchange, kGemvExchangeBytes of 32-bit words carrying split
+// partials.  It is zero before a workspace's first use, every GEMV call leaves
+// it zero again (the workgroup that sums a column group's partials clears what
+// it consumed) and no other kernel writes it.  One workspace therefore serves
+// calls of any shape and row count in turn, when it is as large as each needs.
+// A GEMV whose partials would not fit the exchange runs as a GEMM instead.  The
+// GEMM splits k only while it has fewer than kGemmSplitTiles output tiles; a
+// second kernel sums its split partials.
 constexpr size_t kGemmSplitTiles = 512;
-constexpr size_t kCounterFloor = 512;
 constexpr size_t kGemvExchangeBytes = (size_t)16 << 20;
-inline size_t counter_slots(size_t n) { return n / 128 > kCounterFloor ? n / 128 : kCounterFloor; }
-inline size_t counter_region_bytes(size_t n) { return (counter_slots(n) * 8 + 255) & ~(size_t)255; }
-inline size_t exchange_offset(size_t n) { return counter_region_bytes(n); }
-// bytes every workspace starts with: sync words and the exchange
-inline size_t shared_prefix_bytes(size_t n) { return counter_region_bytes(n) + kGemvExchangeBytes; }
+// bytes every workspace starts with: the exchange
+constexpr size_t kSharedPrefixBytes = kGemvExchangeBytes;
 
 // Up to kGemvMaxTargets matrices that share k, the bit rate, the codebook and x,
 // served by one GEMV launch: column groups [nb_end[i-1], nb_end[i]) belong to
@@ -62,12 +54,12 @@ struct DecodeBatch {
 
 struct GemvPlan {
     int nbs, kbs, splits, nkw;  // nkw: largest kb count of a split
-    size_t counters_off, partials_off, exchange_bytes, dummy_off, xpre_off, bytes;
+    size_t partials_off, exchange_bytes, dummy_off, xpre_off, bytes;
     bool fits;  // the partials fit the exchange (else the call runs as a GEMM)
 };
 struct GemmPlan {
     int nbs, kbs, bm, mtiles, splits;  // bm: rows per workgroup tile (128, 256 or 512)
-    size_t counters_off, xh_off, partials_off, exps_off, bytes;
+    size_t xh_off, partials_off, exps_off, bytes;
 };
 
 GemvPlan gemv_plan(size_t k, size_t n, size_t rows);

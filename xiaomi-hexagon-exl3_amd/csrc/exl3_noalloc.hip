@@ -23,9 +23,9 @@ std::mutex g_scratch_mutex;
 void *g_scratch_ptr[kMaxDevices];  // device address of `scratch` on each device, or null
 
 // The current device's scratch address.  On a device's first call the array's
-// split-K sync words and exchange are cleared on `stream` with a fill kernel (no
-// hipMemsetAsync, so a first call under capture stays replay-safe); every later
-// call finds them zero again because each GEMV call leaves them so.
+// split-K exchange is cleared on `stream` with a fill kernel (no hipMemsetAsync,
+// so a first call under capture stays replay-safe); every later call finds it
+// zero again because each GEMV call leaves it so.
 exl3_status scratch_of_current_device(hipStream_t stream, void **out) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return EXL3_HIP_ERROR;
@@ -33,9 +33,7 @@ exl3_status scratch_of_current_device(hipStream_t stream, void **out) {
     if (!g_scratch_ptr[dev]) {
         void *p = nullptr;
         if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return EXL3_HIP_ERROR;
-        if (exl3k::launch_zero(p, exl3k::shared_prefix_bytes((size_t)exl3k::kCounterFloor * 128), stream) !=
-            hipSuccess)
-            return EXL3_HIP_ERROR;
+        if (exl3k::launch_zero(p, exl3k::kSharedPrefixBytes, stream) != hipSuccess) return EXL3_HIP_ERROR;
         g_scratch_ptr[dev] = p;
     }
     *out = g_scratch_ptr[dev];
@@ -49,9 +47,7 @@ extern "C" exl3_status exl3_hip_mul_mat_noalloc(const void *records, unsigned bi
                                                 size_t x_row_stride, void *y, exl3_dtype yt, size_t y_row_stride,
                                                 hipStream_t stream) {
     if (!exl3_hip_supports_mul_mat(bits, codebook, k, n, rows, xt, yt)) return EXL3_INVAL_PARAMS;
-    // the shared counter layout covers n <= 128 * kCounterFloor; wider layers and
     // workspaces beyond the array are refused before anything is enqueued
-    if (n > (size_t)exl3k::kCounterFloor * 128) return EXL3_INVAL_PARAMS;
     if (exl3_hip_mul_mat_workspace_bytes(k, n, rows) > kNoallocScratchBytes) return EXL3_WORKSPACE_TOO_SMALL;
     void *ws = nullptr;
     const exl3_status st = scratch_of_current_device(stream, &ws);
