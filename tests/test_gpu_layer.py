@@ -86,6 +86,18 @@ def test_gemm_rows(amd, oracle, rows):
     assert_layer_close(run(amd, dev(rec), bits, k, n, x), ref, what=f"GEMM rows={rows}")
 
 
+@pytest.mark.parametrize("k,n,rows", [(1024, 384, 64), (2048, 640, 48), (512, 384, 40)])
+def test_gemm_64_row_tiles(amd, oracle, k, n, rows):
+    """Rows 33..64 run 64-row tiles (2 row waves x 4 column quarters), which
+    always split k; at k = 512 no split is possible (four records per split at
+    least) and the call runs the 128-row tile without one."""
+    bits = 3
+    rec = make_layer(410 + rows, k, n, bits)
+    x = synth.activations(411 + rows, rows, k)
+    ref = oracle.mul_mat(rec, bits, 2, k, n, x, threads=THREADS)
+    assert_layer_close(run(amd, dev(rec), bits, k, n, x), ref, what=f"GEMM k={k} n={n} rows={rows}")
+
+
 def test_c5_prefill_sampled(amd, oracle):
     """M=512 rows against 4096 x 14336 at 4 bits; 8 sampled rows against the oracle,
     all rows against the GEMV path on the same inputs."""
