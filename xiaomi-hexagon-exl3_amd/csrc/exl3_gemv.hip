@@ -157,6 +157,10 @@ __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu
             if constexpr (XF16) __builtin_memcpy(&xr[q][0], (const uint16_t *)x + xi, 16);
             else __builtin_memcpy(&xr[q][0], (const float *)x + xi, 32);
         }
+        // the first weight-ring slot right behind the activation loads: its
+        // latency then passes under this prep's H128 work (the one-block prep
+        // below is too short for that and issues it after the barrier)
+        load_chunk<K>(group_src(0), buf[0]);
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
             if (4 * q * W + wave < nblk) {  // uniform in the wave: the DPP stages see every lane
@@ -278,8 +282,9 @@ __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu
     }
     const float sv0 = half_bits_to_float(svp[lane]), sv1 = half_bits_to_float(svp[lane + 64]);
     __syncthreads();
+    if (MODE == 2 || nblk <= W) load_chunk<K>(group_src(0), buf[0]);  // not issued by the prep
 #pragma unroll
-    for (int d = 0; d < D; ++d) load_chunk<K>(group_src(d), buf[d]);
+    for (int d = 1; d < D; ++d) load_chunk<K>(group_src(d), buf[d]);
 
     // 4. decode + MFMA.  B operand lane l: m = l % 16 -> (hl, row) = (m / 8, m % 8),
     // k group l / 16; rows >= `rows` read the last row (their columns are discarded)
