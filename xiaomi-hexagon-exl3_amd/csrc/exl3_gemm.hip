@@ -504,12 +504,14 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const uint16_t *__rest
 #pragma unroll
         for (int q = 0; q < SB; ++q)
             if (sp0 + q < splits) {
+                // 2^ex is exact and so is the product of a half by it: one fused
+                // rounding per add, the same sum as scaling first and then adding
+                const float sc = __builtin_amdgcn_ldexpf(1.0f, ex[q]);
                 const uint32_t w[4] = {in[q].x, in[q].y, in[q].z, in[q].w};
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const float v =
-                        __builtin_amdgcn_ldexpf(half_bits_to_float((uint16_t)(w[e >> 1] >> (16 * (e & 1)))), ex[q]);
-                    t[e] = sp0 + q == 0 ? v : t[e] + v;
+                    const float h = half_bits_to_float((uint16_t)(w[e >> 1] >> (16 * (e & 1))));
+                    t[e] = sp0 + q == 0 ? h * sc : __builtin_fmaf(h, sc, t[e]);
                 }
             }
     }
