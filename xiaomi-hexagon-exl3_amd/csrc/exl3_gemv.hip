@@ -84,6 +84,12 @@ __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu
     // grid (column group, split): no division on the way to the first loads.
     // Split s owns kq + (s < kr) records from kb0 (kq = kbs / splits, kr = kbs % splits)
     const int nb = blockIdx.x, s = blockIdx.y;
+    // The 9..16-row prep (hi and lo fragments of up to 16 rows) is long enough
+    // that, at equal priority, a CU's second workgroup runs it mostly in the
+    // issue gaps of the first one's decode (the older waves issue first): raised
+    // until the prep barrier it no longer trails by microseconds (rows 12 and 16
+    // -1.3 to -1.9 us per call; no gain at 8 rows or fewer, a loss at 17..32)
+    if constexpr (MODE == 1) __builtin_amdgcn_s_setprio(1);
     const int kb0 = s * kq + (s < kr ? s : kr), kb1 = kb0 + kq + (s < kr ? 1 : 0);
     const int nkb = kb1 - kb0;
     // the matrix of column group nb (targets share k, x and the bit rate)
@@ -282,6 +288,7 @@ __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu
     }
     const float sv0 = half_bits_to_float(svp[lane]), sv1 = half_bits_to_float(svp[lane + 64]);
     __syncthreads();
+    if constexpr (MODE == 1) __builtin_amdgcn_s_setprio(0);
     if (MODE == 2 || nblk <= W) load_chunk<K>(group_src(0), buf[0]);  // not issued by the prep
 #pragma unroll
     for (int d = 1; d < D; ++d) load_chunk<K>(group_src(d), buf[d]);
