@@ -135,7 +135,8 @@ int exl3_hip_supports_op(exl3_op op, const exl3_tensor_info *dst, const exl3_ten
 }
 
 // The largest plan over every row count 1..rows, so one workspace serves all
-// smaller calls of the same (k, n) in turn (plans share the counter region).
+// smaller calls of the same (k, n) in turn (every plan starts with the same
+// exchange region).
 size_t exl3_hip_mul_mat_workspace_bytes(size_t k, size_t n, size_t rows) {
     if (!valid_matrix(k, n, 128) || rows < 1 || rows > kMaxRows) return 0;
     size_t need = 0;

@@ -1,8 +1,8 @@
 // exl3_gemv.hip -- the EXL3 layer at rows 1..32 on gfx950 (gemv_kernel,
 // gemv_xprep_kernel): each lane decodes 32 trellis positions of a tile straight
 // into fp16 MFMA A-fragments (W^T), v_mfma_f32_16x16x32_f16 accumulates in fp32;
-// split-K partials are reduced in fixed order by the last workgroup of each
-// 128-column group, which applies H128 and sv.
+// split-K partials are reduced in fixed order by the last split's workgroup of
+// each 128-column group, which applies H128 and sv.
 // Reference semantics: src/exl3-ggml.cpp:51-92.
 #include <hip/hip_runtime.h>
 
@@ -39,8 +39,9 @@ namespace exl3k {
 //      otherwise) and D2 (32 c2 + 8 + i; 32 c2 + 16 + i).  D[n][m]: lane l holds
 //      m = l % 16, n = 4 (l / 16) + e.
 //   4. epilogue: hi + lo, the P partials of each column pair summed in LDS;
-//      split-K partials are reduced in split order by the last workgroup of
-//      the column group, which applies H128 and sv (src/exl3-ggml.cpp:84-90).
+//      split-K partials are reduced in split order by the workgroup of the
+//      column group's last split, which applies H128 and sv
+//      (src/exl3-ggml.cpp:84-90).
 template <int K>
 struct GemvStream {
     static constexpr int DEPTH = K <= 2 ? 12 : (K <= 4 ? 8 : 4);  // groups in flight per wave
