@@ -65,8 +65,10 @@ typedef enum exl3_layout {
 unsigned exl3_hip_version(void);
 const char *exl3_hip_status_string(exl3_status status);
 
-/* Largest row count served by the register-decode GEMV kernel; larger row
- * counts use the LDS-decode MFMA GEMM kernel. */
+/* Largest row count served by the register-decode GEMV kernel (32): a grouped
+ * call (exl3_hip_mul_mat_group) of at most this many rows is one GEMV launch.
+ * exl3_hip_mul_mat runs the GEMV up to 24 rows and the LDS-decode MFMA GEMM
+ * kernel above, where the GEMM is the faster of the two. */
 size_t exl3_hip_gemv_max_rows(void);
 
 /* 1 when exl3_hip_mul_mat accepts this problem: bits 1..8, codebook 0..2,
@@ -120,9 +122,9 @@ int exl3_hip_supports_op(exl3_op op, const exl3_tensor_info *dst, const exl3_ten
  * before its first use (exl3_hip_workspace_init).  One workspace serves any
  * sequence of calls when it holds at least exl3_hip_mul_mat_workspace_bytes(k,
  * n, rows) of every one of them; calls that share one must not run concurrently
- * (order them on one stream).  A call of at most exl3_hip_gemv_max_rows() rows
- * whose split-K partials would not fit the 16 MiB runs the GEMM path (k * n
- * above about 134 M weights at 32 rows). */
+ * (order them on one stream).  A GEMV call whose split-K partials would not fit
+ * the 16 MiB runs the GEMM path instead (k * n above about 134 M weights at 32
+ * rows). */
 size_t exl3_hip_mul_mat_workspace_bytes(size_t k, size_t n, size_t rows);
 exl3_status exl3_hip_workspace_init(void *workspace, size_t workspace_bytes, hipStream_t stream);
 

@@ -62,11 +62,11 @@ def test_all_rates_and_codebooks(amd, oracle, bits):
             assert_layer_close(run(amd, rd, bits, k, n, x, cb), ref, what=f"bits={bits} cb={cb} rows={rows}")
 
 
-@pytest.mark.parametrize("rows", [1, 2, 4, 8, 9, 12, 16, 17, 24, 32])
+@pytest.mark.parametrize("rows", [1, 2, 4, 8, 9, 12, 16, 17, 24, 25, 32])
 def test_c3_full_size_gemv(amd, oracle, rows):
-    """4096 x 14336 at 4 bits (k=14336 in, n=4096 out), ragged decode batches up to the
-    GEMV's 32 rows (rows 9..16 use its second block of MFMA columns, rows 17..32 fp16
-    activations prepared once per call)"""
+    """4096 x 14336 at 4 bits (k=14336 in, n=4096 out), ragged decode batches up to 32
+    rows: the GEMV to 24 rows (rows 9..16 use its second block of MFMA columns, rows
+    17..24 fp16 activations prepared once per call), the GEMM's 64-row tiles above"""
     k, n, bits = 14336, 4096, 4
     rec = make_layer(303, k, n, bits)
     x = synth.activations(304 + rows, rows, k)

@@ -134,9 +134,10 @@ int exl3_hip_supports_op(exl3_op op, const exl3_tensor_info *dst, const exl3_ten
     return 0;
 }
 
-// The largest plan over every row count 1..rows, so one workspace serves all
-// smaller calls of the same (k, n) in turn (every plan starts with the same
-// exchange region).
+// The largest plan over every row count 1..rows and both paths a row count can
+// take (rows 25..32: the GEMM for one matrix, the GEMV for a group of them), so
+// one workspace serves all smaller calls of the same (k, n) in turn (every plan
+// starts with the same exchange region).
 size_t exl3_hip_mul_mat_workspace_bytes(size_t k, size_t n, size_t rows) {
     if (!valid_matrix(k, n, 128) || rows < 1 || rows > kMaxRows) return 0;
     size_t need = 0;
@@ -147,7 +148,7 @@ size_t exl3_hip_mul_mat_workspace_bytes(size_t k, size_t n, size_t rows) {
     }
     // GEMM plans: the largest row count of each (tile height, m-tile count) run;
     // r_hi >= r, so every pass moves on
-    for (size_t r = exl3k::kGemvMaxRows + 1; r <= rows;) {
+    for (size_t r = exl3k::kGemvSingleMaxRows + 1; r <= rows;) {
         const int bm = exl3k::gemm_tile_rows(r);
         size_t r_hi = std::min(rows, (r + bm - 1) / bm * bm);
         while (exl3k::gemm_tile_rows(r_hi) != bm) --r_hi;
@@ -170,7 +171,7 @@ static exl3_status mul_mat_impl(const void *records, unsigned bits, unsigned cod
     if (!records || !x || !y || !aligned(records, 16)) return EXL3_INVAL_PARAMS;
     if (!aligned(x, dtype_size(xt)) || !aligned(y, dtype_size(yt))) return EXL3_INVAL_PARAMS;
     if (x_row_stride < k || y_row_stride < n) return EXL3_INVAL_PARAMS;
-    const bool gemv = exl3k::gemv_serves(k, n, rows);
+    const bool gemv = rows <= (size_t)exl3k::kGemvSingleMaxRows && exl3k::gemv_serves(k, n, rows);
     const size_t need = exl3_hip_mul_mat_workspace_bytes(k, n, rows);
     if (workspace) {
         if (!aligned(workspace, 256)) return EXL3_INVAL_PARAMS;
@@ -227,7 +228,9 @@ exl3_status exl3_hip_mul_mat_group(const exl3_matrix_desc *mats, size_t count, u
         n_total += m.n;
     }
     if (!x || !aligned(x, dtype_size(xt)) || x_row_stride < k || n_total > kMaxDim) return EXL3_INVAL_PARAMS;
-    if (!exl3k::gemv_serves(k, n_total, rows)) {  // GEMM: one call per matrix, each a full-size launch
+    // GEMM (or, for one matrix above the single-matrix GEMV rows, whichever
+    // exl3_hip_mul_mat picks): one call per matrix, each a full-size launch
+    if (!exl3k::gemv_serves(k, n_total, rows) || (count == 1 && rows > (size_t)exl3k::kGemvSingleMaxRows)) {
         for (size_t i = 0; i < count; ++i) {
             const exl3_status st = exl3_hip_mul_mat(mats[i].records, bits, codebook, k, mats[i].n, x, xt, rows,
                                                     x_row_stride, mats[i].y, yt, mats[i].y_row_stride, workspace,
