@@ -194,12 +194,12 @@ def main():
 
     extra = {}
     if not args.only_gemv:
-        for r in (2, 4, 8, 16, 24):   # 16, 24: continuous batching past 8 requests (GEMV up to 24 rows)
+        for r in (2, 4, 8, 16):   # 16: continuous batching past 8 requests (GEMV up to 16 rows)
             ms, _ = timed(r, xs[r], args.steps, args.warmup)
             gbps = algo_bytes(K_IN, N_OUT, BITS, r) / (ms * 1e-3) / 1e9
             extra[f"gemv_rows{r}"] = {"gbps": round(gbps, 1), "call_us": round(ms * 1e3, 2),
                                       "frac_hbm": round(gbps / HBM_PEAK_GBPS, 4)}
-        for r in (32, 33, 64, 128):   # past the GEMV: the GEMM's 64-row (up to 64) and 128-row tiles
+        for r in (24, 32, 33, 64, 128):   # past the GEMV: the GEMM's 32-, 64- and 128-row tiles
             ms, _ = timed(r, xs[r], max(36, args.steps // 2), args.warmup)
             gbps = algo_bytes(K_IN, N_OUT, BITS, r) / (ms * 1e-3) / 1e9
             tflops = 2.0 * r * K_IN * N_OUT / (ms * 1e-3) / 1e12

@@ -65,8 +65,8 @@ def test_all_rates_and_codebooks(amd, oracle, bits):
 @pytest.mark.parametrize("rows", [1, 2, 4, 8, 9, 12, 16, 17, 24, 25, 32])
 def test_c3_full_size_gemv(amd, oracle, rows):
     """4096 x 14336 at 4 bits (k=14336 in, n=4096 out), ragged decode batches up to 32
-    rows: the GEMV to 24 rows (rows 9..16 use its second block of MFMA columns, rows
-    17..24 fp16 activations prepared once per call), the GEMM's 64-row tiles above"""
+    rows: the GEMV to 16 rows (rows 9..16 use its second block of MFMA columns), the
+    GEMM's 32-row tiles above"""
     k, n, bits = 14336, 4096, 4
     rec = make_layer(303, k, n, bits)
     x = synth.activations(304 + rows, rows, k)
@@ -86,11 +86,13 @@ def test_gemm_rows(amd, oracle, rows):
     assert_layer_close(run(amd, dev(rec), bits, k, n, x), ref, what=f"GEMM rows={rows}")
 
 
-@pytest.mark.parametrize("k,n,rows", [(1024, 384, 64), (2048, 640, 48), (512, 384, 40)])
-def test_gemm_64_row_tiles(amd, oracle, k, n, rows):
-    """Rows 33..64 run 64-row tiles (2 row waves x 4 column quarters), which
-    always split k; at k = 512 no split is possible (four records per split at
-    least) and the call runs the 128-row tile without one."""
+@pytest.mark.parametrize("k,n,rows", [(1024, 384, 64), (2048, 640, 48), (512, 384, 40), (1024, 384, 17),
+                                      (2048, 640, 32), (512, 384, 24)])
+def test_gemm_short_row_tiles(amd, oracle, k, n, rows):
+    """Rows 17..32 run 32-row tiles (4 column quarters), rows 33..64 64-row tiles
+    (2 row waves x 4 column quarters); both always split k, and at k = 512 no
+    split is possible (four records per split at least), so the call runs the
+    128-row tile without one."""
     bits = 3
     rec = make_layer(410 + rows, k, n, bits)
     x = synth.activations(411 + rows, rows, k)

@@ -44,7 +44,7 @@ def test_noalloc_matches_mul_mat_on_consecutive_calls(amd):
     cases = [  # (k, n, bits, rows) in call order: each second call of a pair is smaller
         (14336, 4096, 4, 8), (14336, 4096, 4, 3),     # GEMV, then a smaller GEMV
         (4096, 2048, 4, 64), (4096, 2048, 4, 1),      # GEMM, then a GEMV on the same array
-        (2048, 6144, 3, 24), (2048, 6144, 3, 17),     # prepared-activation GEMV
+        (2048, 6144, 3, 24), (2048, 6144, 3, 17),     # GEMM, 32-row tiles
         (1024, 512, 5, 300), (1024, 512, 5, 33),      # two GEMM m-tiles, then one
         (512, 65664, 2, 40), (512, 65664, 2, 2),      # n above 65536: GEMM, then GEMV
     ]

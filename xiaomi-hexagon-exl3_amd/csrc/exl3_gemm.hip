@@ -233,7 +233,8 @@ __device__ __forceinline__ void gemm_rows_out(float (&t)[4][NE], int lane, int r
 // CH column parts: with CH = 2 (4) the W waves are W / CH row waves x CH column
 // parts, each wave owning 32 RB rows x 128 / CH columns (4 / CH accumulator
 // blocks per row block), so that a 128-row (64-row) tile runs two waves per
-// SIMD; such a tile always has a k split (its epilogue writes partials only).
+// SIMD and a 32-row tile four waves per workgroup; such a tile always has a k
+// split (its epilogue writes partials only).
 template <int K, int CB, int RB, int W, int NSG, int XD, int CH>
 __global__ __launch_bounds__(W * 64) void gemm_kernel(
     const uint8_t *__restrict__ records, int kbs, int nbs, int mtiles, int splits, int kq, int kr,
@@ -552,15 +553,18 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const uint16_t *__rest
     }
 }
 
-// Tile heights: 64 rows (8 waves: 2 row waves x 4 column quarters), 128 (8 waves:
-// 4 x 2 column halves with a k split, else 4 waves of one 32-row block each), 256
-// (4 waves, two blocks), 512 (8 waves, two blocks): above 256 rows one 512-row
-// tile decodes each record once for all rows where two 256-row tiles decode it
-// twice.  Up to 64 rows the 64-row tile halves the padded MFMA work and
-// activation loads of a 128-row one (rows 33..64 at k = 14336, n = 4096: 33.5 ->
-// 27.7 us per call); two 64-row tiles for rows 65..128 decode every record twice
-// and are slower (42 against 34 us).
-int gemm_tile_rows(size_t rows) { return rows <= 64 ? 64 : rows <= 128 ? 128 : rows <= 256 ? 256 : 512; }
+// Tile heights: 32 rows (4 waves: 4 column quarters), 64 rows (8 waves: 2 row
+// waves x 4 column quarters), 128 (8 waves: 4 x 2 column halves with a k split,
+// else 4 waves of one 32-row block each), 256 (4 waves, two blocks), 512 (8
+// waves, two blocks): above 256 rows one 512-row tile decodes each record once
+// for all rows where two 256-row tiles decode it twice.  The short tiles cut
+// the padded MFMA work and activation loads of a 128-row one (rows 33..64 at
+// k = 14336, n = 4096: 33.5 -> 27.7 us per call; rows 17..32 on 32-row tiles
+// 22.7 us against 24.5 on 64-row ones); two 64-row tiles for rows 65..128
+// decode every record twice and are slower (42 against 34 us).
+int gemm_tile_rows(size_t rows) {
+    return rows <= 32 ? 32 : rows <= 64 ? 64 : rows <= 128 ? 128 : rows <= 256 ? 256 : 512;
+}
 
 static GemmPlan gemm_plan_bm(size_t k, size_t n, size_t rows, int bm) {
     GemmPlan p{};
@@ -574,7 +578,7 @@ static GemmPlan gemm_plan_bm(size_t k, size_t n, size_t rows, int bm) {
     int s = tiles >= (int)kGemmSplitTiles ? 1 : (kGemmTargetWgs + tiles - 1) / tiles;
     const int smax = p.kbs / 4 > 0 ? p.kbs / 4 : 1;
     s = s < 1 ? 1 : (s > smax ? smax : s);
-    if (p.bm == 64 && s == 1) return gemm_plan_bm(k, n, rows, 128);  // the 64-row tile needs a split
+    if (p.bm < 128 && s == 1) return gemm_plan_bm(k, n, rows, 128);  // the 32/64-row tiles need a split
     p.splits = s;
     size_t off = kSharedPrefixBytes;  // the GEMM leaves the GEMV exchange alone
     p.xh_off = off;
@@ -596,7 +600,7 @@ static void launch_gemm_tiles(const uint8_t *rec, size_t k, uint16_t *xh, size_t
                               size_t y_stride, uint8_t *ws, const GemmPlan &p, hipStream_t stream, const void *res,
                               size_t res_stride) {
     constexpr int WR = W / CH;  // the reduction sees the row waves
-    static_assert(32 * RB * WR == 64 || 32 * RB * WR == 128 || 32 * RB * WR == 256 || 32 * RB * WR == 512,
+    static_assert(32 * RB * WR == 32 || 32 * RB * WR == 64 || 32 * RB * WR == 128 || 32 * RB * WR == 256 || 32 * RB * WR == 512,
                   "tile height");
     const dim3 grid((unsigned)(p.mtiles * p.nbs * p.splits)), block(W * 64);
     uint16_t *part = (uint16_t *)(ws + p.partials_off);
@@ -615,7 +619,9 @@ template <int K, int CB>
 static void launch_gemm_kc(const uint8_t *rec, size_t k, uint16_t *xh, size_t rows, void *y, int y_f16,
                            size_t y_stride, uint8_t *ws, const GemmPlan &p, hipStream_t stream, const void *res,
                            size_t res_stride) {
-    if (p.bm == 64)  // 8 waves: 2 row waves x 4 column quarters (the plan gives it a split)
+    if (p.bm == 32)  // 4 waves: 4 column quarters (the plan gives it a split)
+        launch_gemm_tiles<K, CB, 1, 4, 0, 8, 4>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream, res, res_stride);
+    else if (p.bm == 64)  // 8 waves: 2 row waves x 4 column quarters (the plan gives it a split)
         launch_gemm_tiles<K, CB, 1, 8, 0, 8, 4>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream, res, res_stride);
     else if (p.bm == 128 && p.splits > 1)  // 8 waves: 4 row waves x 2 column halves, two waves per SIMD
         launch_gemm_tiles<K, CB, 1, 8, 0, 8, 2>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream, res, res_stride);

@@ -11,13 +11,14 @@ namespace exl3k {
 
 // GEMV: hi/lo fp16 halves of 8 rows per 16 MFMA columns (one block up to 8 rows, two
 // up to 16); 17..32 rows as two blocks of 16 fp16 rows prepared once per call.
-// A single matrix above kGemvSingleMaxRows rows runs the GEMM (64-row tiles),
-// which is flat in the row count from there and faster from about 20..24 rows
-// on (k = 14336, n = 4096 at 32 rows: 26.6 against 30.6 us; k = 2048, n = 6144:
-// 15.0 against 17.6 us); a grouped call keeps its one GEMV launch up to
-// kGemvMaxRows rows (q/k/v at 32 rows: 18 us against 41 us for three GEMMs).
+// A single matrix above kGemvSingleMaxRows rows runs the GEMM (32-row tiles up to
+// 32 rows), which is flat in the row count from there and as fast from about 16
+// rows on (k = 14336, n = 4096: 22.7 us for rows 17..32 against the GEMV's
+// 24.5 us at 20 rows and 26.1 at 24); a grouped call keeps its one GEMV launch
+// up to kGemvMaxRows rows (q/k/v at 32 rows: 18 us against 41 us for three
+// GEMM calls).
 constexpr int kGemvMaxRows = 32;
-constexpr int kGemvSingleMaxRows = 24;
+constexpr int kGemvSingleMaxRows = 16;
 constexpr int kGemvWaves = 8;     // waves per GEMV workgroup (a multiple of 4)
 
 // Every plan starts with the same region, which only the GEMV's split-K hand-off
