@@ -67,7 +67,7 @@ const char *exl3_hip_status_string(exl3_status status);
 
 /* Largest row count served by the register-decode GEMV kernel (32): a grouped
  * call (exl3_hip_mul_mat_group) of at most this many rows is one GEMV launch.
- * exl3_hip_mul_mat runs the GEMV up to 16 rows and the LDS-decode MFMA GEMM
+ * exl3_hip_mul_mat runs the GEMV up to 14 rows and the LDS-decode MFMA GEMM
  * kernel above, where the GEMM is the faster of the two. */
 size_t exl3_hip_gemv_max_rows(void);
 

@@ -62,10 +62,10 @@ def test_all_rates_and_codebooks(amd, oracle, bits):
             assert_layer_close(run(amd, rd, bits, k, n, x, cb), ref, what=f"bits={bits} cb={cb} rows={rows}")
 
 
-@pytest.mark.parametrize("rows", [1, 2, 4, 8, 9, 12, 16, 17, 24, 25, 32])
+@pytest.mark.parametrize("rows", [1, 2, 4, 8, 9, 12, 14, 15, 16, 17, 24, 32])
 def test_c3_full_size_gemv(amd, oracle, rows):
     """4096 x 14336 at 4 bits (k=14336 in, n=4096 out), ragged decode batches up to 32
-    rows: the GEMV to 16 rows (rows 9..16 use its second block of MFMA columns), the
+    rows: the GEMV to 14 rows (rows 9..14 use its second block of MFMA columns), the
     GEMM's 32-row tiles above"""
     k, n, bits = 14336, 4096, 4
     rec = make_layer(303, k, n, bits)
@@ -73,7 +73,7 @@ def test_c3_full_size_gemv(amd, oracle, rows):
     ref = oracle.mul_mat(rec, bits, 2, k, n, x, threads=THREADS)
     y = run(amd, dev(rec), bits, k, n, x)
     ma, rl = assert_layer_close(y, ref, what=f"C3 rows={rows}")
-    if rows <= 16:
+    if rows <= 14:  # exl3_hip_mul_mat runs one matrix on the GEMV up to 14 rows (include/exl3_hip.h)
         assert rl < 1e-5  # hi/lo activation split keeps the GEMV at fp32-level accuracy
 
 

@@ -135,7 +135,7 @@ int exl3_hip_supports_op(exl3_op op, const exl3_tensor_info *dst, const exl3_ten
 }
 
 // The largest plan over every row count 1..rows and both paths a row count can
-// take (rows 17..32: the GEMM for one matrix, the GEMV for a group of them), so
+// take (rows 15..32: the GEMM for one matrix, the GEMV for a group of them), so
 // one workspace serves all smaller calls of the same (k, n) in turn (every plan
 // starts with the same exchange region).
 size_t exl3_hip_mul_mat_workspace_bytes(size_t k, size_t n, size_t rows) {

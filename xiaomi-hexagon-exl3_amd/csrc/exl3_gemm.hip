@@ -575,7 +575,11 @@ static GemmPlan gemm_plan_bm(size_t k, size_t n, size_t rows, int bm) {
     const int tiles = p.nbs * p.mtiles;
     // split k only below kGemmSplitTiles tiles; the split partials are summed by
     // gemm_reduce_kernel
-    int s = tiles >= (int)kGemmSplitTiles ? 1 : (kGemmTargetWgs + tiles - 1) / tiles;
+    // 32-row tiles (4 waves, 64 KB of LDS) run two workgroups per CU: twice the
+    // target there (rows 17..32 at k = 14336, n = 4096: 22.7 -> 21.2 us; four
+    // per CU do not fit and were 28.4 us)
+    const int target = p.bm == 32 ? 2 * kGemmTargetWgs : kGemmTargetWgs;
+    int s = tiles >= (int)kGemmSplitTiles ? 1 : (target + tiles - 1) / tiles;
     const int smax = p.kbs / 4 > 0 ? p.kbs / 4 : 1;
     s = s < 1 ? 1 : (s > smax ? smax : s);
     if (p.bm < 128 && s == 1) return gemm_plan_bm(k, n, rows, 128);  // the 32/64-row tiles need a split

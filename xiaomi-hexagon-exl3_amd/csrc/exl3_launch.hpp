@@ -12,13 +12,12 @@ namespace exl3k {
 // GEMV: hi/lo fp16 halves of 8 rows per 16 MFMA columns (one block up to 8 rows, two
 // up to 16); 17..32 rows as two blocks of 16 fp16 rows prepared once per call.
 // A single matrix above kGemvSingleMaxRows rows runs the GEMM (32-row tiles up to
-// 32 rows), which is flat in the row count from there and as fast from about 16
-// rows on (k = 14336, n = 4096: 22.7 us for rows 17..32 against the GEMV's
-// 24.5 us at 20 rows and 26.1 at 24); a grouped call keeps its one GEMV launch
-// up to kGemvMaxRows rows (q/k/v at 32 rows: 18 us against 41 us for three
-// GEMM calls).
+// 32 rows), which is flat in the row count from there (k = 14336, n = 4096:
+// 21.2-21.5 us for rows 14..32, against the GEMV's 21.4 at 14 rows, 22.4 at 16,
+// 24.5 at 20); a grouped call keeps its one GEMV launch up to kGemvMaxRows rows
+// (q/k/v at 32 rows: 18 us against 41 us for three GEMM calls).
 constexpr int kGemvMaxRows = 32;
-constexpr int kGemvSingleMaxRows = 16;
+constexpr int kGemvSingleMaxRows = 14;
 constexpr int kGemvWaves = 8;     // waves per GEMV workgroup (a multiple of 4)
 
 // Every plan starts with the same region, which only the GEMV's split-K hand-off
