@@ -11,7 +11,8 @@ import synth
 from gpu_util import assert_layer_close, dev
 
 pytestmark = pytest.mark.gpu
-CASES = 36
+CASES = 48  # 0..35 over all row counts, 36..47 around the kernel boundaries (14 | 15, 32 | 33, 64)
+BOUNDARY_ROWS = [14, 15, 16, 17, 24, 32, 33, 48, 64]
 
 
 def case(i):
@@ -20,7 +21,7 @@ def case(i):
     n = 128 * int(rng.integers(1, 13))
     bits = int(rng.integers(1, 9))
     cb = int(rng.integers(0, 3))
-    rows = int(rng.choice([1, 2, 3, 5, 7, 8, 9, 13, 31, 64, 129, 257]))
+    rows = int(rng.choice([1, 2, 3, 5, 7, 8, 9, 13, 31, 64, 129, 257] if i < 36 else BOUNDARY_ROWS))
     while k * n * rows > 40_000_000:
         rows = max(1, rows // 2)
     x16 = bool(rng.integers(0, 2))
