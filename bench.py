@@ -114,9 +114,9 @@ def main():
     copies = [rec] + [rec.clone() for _ in range(COPIES - 1)]
     del p
     xs = {r: torch.from_numpy(synth.activations(1000 + r, r, K_IN)).to(dev)
-          for r in (1, 2, 4, 8, 16, 24, 32, 33, 64, 128)}
+          for r in (1, 2, 4, 8, 12, 14, 16, 24, 32, 33, 64, 128)}
     x512 = torch.from_numpy(synth.activations(5000, 512, K_IN)).to(dev)
-    row_set = list(range(1, 9)) + [16, 24, 32, 33, 64, 128, 512]
+    row_set = list(range(1, 9)) + [12, 14, 16, 24, 32, 33, 64, 128, 512]
     ys = {r: torch.empty((r, N_OUT), dtype=torch.float16, device=dev) for r in row_set}
     ws = {r: amd.new_workspace(K_IN, N_OUT, r) for r in row_set}
     torch.cuda.synchronize()
@@ -194,12 +194,12 @@ def main():
 
     extra = {}
     if not args.only_gemv:
-        for r in (2, 4, 8, 16):   # 16: continuous batching past 8 requests (GEMV up to 16 rows)
+        for r in (2, 4, 8, 12, 14):   # 12, 14: continuous batching past 8 requests (GEMV up to 14 rows)
             ms, _ = timed(r, xs[r], args.steps, args.warmup)
             gbps = algo_bytes(K_IN, N_OUT, BITS, r) / (ms * 1e-3) / 1e9
             extra[f"gemv_rows{r}"] = {"gbps": round(gbps, 1), "call_us": round(ms * 1e3, 2),
                                       "frac_hbm": round(gbps / HBM_PEAK_GBPS, 4)}
-        for r in (24, 32, 33, 64, 128):   # past the GEMV: the GEMM's 32-, 64- and 128-row tiles
+        for r in (16, 24, 32, 33, 64, 128):   # past the GEMV: the GEMM's 32-, 64- and 128-row tiles
             ms, _ = timed(r, xs[r], max(36, args.steps // 2), args.warmup)
             gbps = algo_bytes(K_IN, N_OUT, BITS, r) / (ms * 1e-3) / 1e9
             tflops = 2.0 * r * K_IN * N_OUT / (ms * 1e-3) / 1e12
