@@ -49,7 +49,7 @@ def test_graph_matmul_add_semantics(amd, oracle, batch, xname):
     assert np.isfinite(nmse) and nmse < 1e-5
 
 
-@pytest.mark.parametrize("rows", [1, 5, 8, 9, 37, 300])
+@pytest.mark.parametrize("rows", [1, 5, 8, 9, 20, 37, 300])
 def test_fused_add_is_plain_result_plus_residual(amd, rows):
     import torch
     k, n, bits = 1024, 384, 4
