@@ -11,6 +11,10 @@
  *                            declared include/exl3-block.h:46, dispatched from
  *                            ggml_compute_forward_mul_mat (patches/llama-exl3.patch:44-51);
  *                            device twin op_exl3_matmul src/exl3-htp.c:159-232
+ *   exl3_hip_mul_mat_nd   <- ggml_exl3_mul_mat with its row_offset addressing of
+ *                            ggml views (src/exl3-ggml.cpp:11-17, 64, 88)
+ *   exl3_hip_get_rows_nd  <- ggml_exl3_get_rows with its id and row addressing
+ *                            (src/exl3-ggml.cpp:34-36)
  *   exl3_hip_iface_matmul <- exl3_iface_matmul src/hexagon/exl3_service.c:265-305
  *                            (IDL src/hexagon/exl3_iface.idl:13-15): the same layer on the
  *                            upstream tile layout with separate su / sv, fp32 in and out
@@ -42,7 +46,7 @@
 extern "C" {
 #endif
 
-#define EXL3_HIP_VERSION 10000u /* major * 10000 + minor * 100 + patch */
+#define EXL3_HIP_VERSION 10100u /* major * 10000 + minor * 100 + patch */
 
 typedef enum exl3_status {
     EXL3_OK = 0,
@@ -109,10 +113,21 @@ typedef struct exl3_tensor_info {
     unsigned type;     /* ggml type id */
     int64_t ne[4];     /* ggml ne[]: ne[0] is the row length */
     int contiguous;    /* ggml_is_contiguous() */
+    size_t nb[4];      /* ggml nb[]: byte strides of the four dimensions */
 } exl3_tensor_info;
 
 /* dst and src0 are required; src1 is required for MUL_MAT, MUL_MAT_ID and GET_ROWS
- * (NULL there: 0). */
+ * (NULL there: 0).  Beyond the reference's rules, MUL_MAT and GET_ROWS are served
+ * when exl3_hip_mul_mat_nd / exl3_hip_get_rows_nd can address every row of the
+ * views as the reference's row_offset does (src/exl3-ggml.cpp:11-17):
+ *   MUL_MAT   src1 nb[0] = its element size and nb[1..3] multiples of it;
+ *             dst F32, ne = [src0 ne[1], src1 ne[1], src1 ne[2], src1 ne[3]],
+ *             nb[0] = 4, nb[1..3] multiples of 4, no two dst rows overlapping
+ *   GET_ROWS  src1 (ids) ne[3] = 1 and nb[0..2] multiples of 4; dst ne = [src0
+ *             ne[0], src1 ne[0], src1 ne[1], src1 ne[2]], nb[0] = its element
+ *             size, nb[1..3] multiples of it, no two dst rows overlapping
+ * Anything else touching an EXL3 tensor is refused (0), so no view is ever
+ * read or written at addresses other than ggml's. */
 int exl3_hip_supports_op(exl3_op op, const exl3_tensor_info *dst, const exl3_tensor_info *src0,
                          const exl3_tensor_info *src1);
 
@@ -126,7 +141,28 @@ int exl3_hip_supports_op(exl3_op op, const exl3_tensor_info *dst, const exl3_ten
  * the 16 MiB runs the GEMM path instead (k * n above about 134 M weights at 32
  * rows). */
 size_t exl3_hip_mul_mat_workspace_bytes(size_t k, size_t n, size_t rows);
+/* Zero-fills workspace_bytes of a caller workspace; NULL: the internal workspace
+ * of the current device and this stream, if one exists. */
 exl3_status exl3_hip_workspace_init(void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Split-K failure flag of a workspace (NULL: the internal workspace of the current
+ * device and this stream).  A GEMV workgroup that sums split partials waits for each
+ * other split's words a bounded time (2^20 polls per wave, about a second); one
+ * that never arrives gives NaN in the outputs that need it and sets a status word
+ * in the workspace.  A partial may then still arrive after the exchange was
+ * cleared, so while the word is set every GEMV call with that workspace writes NaN
+ * for every output it sums, without waiting; exl3_hip_workspace_init clears it.
+ * *faulted = 1 when the word is set, else 0.  Synchronises the stream.  No
+ * counterpart in the reference, whose ops run on one thread pool per call. */
+exl3_status exl3_hip_workspace_status(const void *workspace, size_t workspace_bytes, int *faulted,
+                                      hipStream_t stream);
+
+/* Test hook for the failure path above, never needed by an engine: spin_limit > 0
+ * replaces the wait budget (polls per wave) and drop_split >= 0 makes the
+ * workgroups of that k split skip storing their partial, so the summing
+ * workgroup's own bounded wait runs out and every kernel still ends normally.
+ * (0, -1) restores the defaults.  Process-wide; not for concurrent use. */
+exl3_status exl3_hip_test_exchange_fault(int spin_limit, int drop_split);
 
 /*
  * y[r][j] = sv[j] * H128( sum_i H128(x[r] * su)[i] * W_hat[i][j] )   (0 <= r < rows)
@@ -204,6 +240,31 @@ exl3_status exl3_hip_mul_mat_group(const exl3_matrix_desc *mats, size_t count, u
                                    size_t k, const void *x, exl3_dtype xt, size_t rows, size_t x_row_stride,
                                    exl3_dtype yt, void *workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* Workspace bytes of an exl3_hip_mul_mat_group call: the most any row count
+ * 1..rows needs, whether the call runs as one GEMV launch over the total width or
+ * as one exl3_hip_mul_mat per matrix (a narrower matrix may need more split
+ * partials than the total width does).  0 for invalid arguments. */
+size_t exl3_hip_mul_mat_group_workspace_bytes(size_t k, const size_t *n, size_t count, size_t rows);
+
+/* The ggml op on ggml views, replacing ggml_exl3_mul_mat (src/exl3-ggml.cpp:51-92)
+ * with its row addressing: row r = i1 + ne[1] (i2 + ne[2] i3) of x starts at byte
+ * i1 nb[1] + i2 nb[2] + i3 nb[3] of x, and its output row at the same indices of y
+ * (row_offset, src/exl3-ggml.cpp:11-17, used at :64 and :88).
+ *   x_info  type EXL3_GGML_TYPE_F32 or _F16, ne[0] = k, nb[0] = its element size,
+ *           nb[1..3] multiples of it, in any order (permuted and sliced views)
+ *   y_info  type F32 or F16, ne[0] = n, ne[1..3] = x's, nb[0] = its element size,
+ *           nb[1..3] multiples of it, no two rows overlapping
+ *   (the contiguous fields are not read)
+ * The longest run of row dimensions that both views step through with one
+ * stride is one exl3_hip_mul_mat call; the other dimensions loop over such calls.
+ * workspace: >= exl3_hip_mul_mat_workspace_bytes(k, n, ne[1] ne[2] ne[3]), or NULL.
+ * Each row is within exl3_hip_mul_mat's tolerance (which kernel serves a row
+ * depends on how many rows share its call). */
+exl3_status exl3_hip_mul_mat_nd(const void *records, unsigned bits, unsigned codebook, size_t k, size_t n,
+                                const void *x, const exl3_tensor_info *x_info, void *y,
+                                const exl3_tensor_info *y_info, void *workspace, size_t workspace_bytes,
+                                hipStream_t stream);
+
 /* Decode packed weights to row-major fp16 bits out[k][column_count] for
  * columns [first_column, first_column + column_count), bit-exact with
  * exl3::decode_inner_slice.  UPSTREAM_TILES: k, n, first and count multiples
@@ -250,6 +311,17 @@ exl3_status exl3_hip_reconstruct(const void *src, exl3_layout layout, const uint
 exl3_status exl3_hip_get_rows(const void *records, unsigned bits, unsigned codebook, size_t k, size_t n,
                               const int32_t *ids, size_t count, void *out, exl3_dtype ot, size_t out_row_stride,
                               int *bad_ids, hipStream_t stream);
+
+/* GET_ROWS on ggml views (ggml_exl3_get_rows, src/exl3-ggml.cpp:19-49): id
+ * r = i0 + ne[0] (i1 + ne[1] i2) is read at byte i0 nb[0] + i1 nb[1] + i2 nb[2] of
+ * ids, and its row written at byte i0 nb[1] + i1 nb[2] + i2 nb[3] of out (:34-36).
+ *   ids_info  type EXL3_GGML_TYPE_I32, ne[3] = 1, nb[0..2] multiples of 4
+ *   out_info  type F32 or F16, ne = [k, ids ne[0], ids ne[1], ids ne[2]], nb[0] =
+ *             its element size, nb[1..3] multiples of it, no two rows overlapping
+ * Otherwise as exl3_hip_get_rows; no ids (a zero ne) is a no-op. */
+exl3_status exl3_hip_get_rows_nd(const void *records, unsigned bits, unsigned codebook, size_t k, size_t n,
+                                 const int32_t *ids, const exl3_tensor_info *ids_info, void *out,
+                                 const exl3_tensor_info *out_info, int *bad_ids, hipStream_t stream);
 
 /* out[i] = fp16 codebook value of states[i], bit-exact with exl3::decode_codebook. */
 exl3_status exl3_hip_codebook(const uint16_t *states, size_t count, unsigned codebook, uint16_t *out,

@@ -30,7 +30,7 @@ def test_library_loads_and_exports_c_abi():
     missing = [f for f in declared if f not in syms]
     assert not missing, missing
     assert set(amd.EXPORTS) == set(declared)
-    assert amd.lib().exl3_hip_version() == 10000
+    assert amd.lib().exl3_hip_version() == 10100
     assert amd.lib().exl3_hip_gemv_max_rows() == 32
 
 
@@ -152,3 +152,78 @@ def test_ggml_op_predicates():
     assert a.supports_op(a.OP_CPY, T(Q4, [k, n], False), w) == 0
     assert a.supports_op(a.OP_SET_ROWS, T(Q4, [k, n]), T(F32, [k, 3]), T(I32, [3])) == 0
     assert a.supports_op(a.OP_CPY, T(F16, [k, n]), T(F32, [k, n])) == -1
+
+
+def test_ggml_op_predicates_views():
+    """MUL_MAT and GET_ROWS on ggml views: served when every row is addressable as
+    the reference's row_offset addresses it (src/exl3-ggml.cpp:11-17, 34-36) by
+    exl3_hip_mul_mat_nd / exl3_hip_get_rows_nd; refused when a row cannot be (an
+    element stride inside the row, a stride that is not a whole element), when two
+    output rows share bytes, or when dst's shape does not follow src0 and src1."""
+    import conftest
+    a = conftest.load_amd()
+    T = a.TensorInfo.of
+    F32, F16, I32, Q4 = a.GGML_F32, a.GGML_F16, a.GGML_I32, 43
+    k, n = 2048, 6144
+    w = T(Q4, [k, n])
+    # permuted and sliced 3-D activations: served (one call per non-uniform slice)
+    perm = T(F16, [k, 2, 3], nb=[2, 2 * k * 3, 2 * k, 2 * k * 6])
+    assert a.supports_op(a.OP_MUL_MAT, T(F32, [n, 2, 3]), w, perm) == 1
+    sliced = T(F32, [k, 3, 2], nb=[4, 4 * k, 4 * k * 5, 4 * k * 10])
+    assert a.supports_op(a.OP_MUL_MAT, T(F32, [n, 3, 2]), w, sliced) == 1
+    # a permuted dst whose rows do not overlap: served
+    assert a.supports_op(a.OP_MUL_MAT, T(F32, [n, 2, 3], nb=[4, 4 * n * 3, 4 * n, 4 * n * 6]), w, perm) == 1
+    # refused: element stride inside a row, a stride of half an element, overlapping dst rows,
+    # dst shape not [ne01, ne11, ne12, ne13]
+    assert a.supports_op(a.OP_MUL_MAT, T(F32, [n, 4]), w, T(F32, [k, 4], nb=[8, 8 * k, 32 * k, 32 * k])) == 0
+    assert a.supports_op(a.OP_MUL_MAT, T(F32, [n, 4]), w, T(F16, [k, 4], nb=[2, 2 * k + 1, 8 * k + 4, 0])) == 0
+    assert a.supports_op(a.OP_MUL_MAT, T(F32, [n, 4], nb=[4, 2 * n, 8 * n, 8 * n]), w, T(F32, [k, 4])) == 0
+    assert a.supports_op(a.OP_MUL_MAT, T(F32, [n, 2, 2], nb=[4, 4 * n, 6 * n, 12 * n]), w,
+                         T(F32, [k, 2, 2])) == 0   # rows 1 and 2 overlap (stride 1.5 rows)
+    assert a.supports_op(a.OP_MUL_MAT, T(F32, [n, 4], nb=[8, 8 * n, 0, 0]), w, T(F32, [k, 4])) == 0
+    assert a.supports_op(a.OP_MUL_MAT, T(F32, [n, 5]), w, T(F32, [k, 4])) == 0
+    assert a.supports_op(a.OP_MUL_MAT, T(F32, [n + 128, 4]), w, T(F32, [k, 4])) == 0
+    assert a.supports_op(a.OP_MUL_MAT, T(F32, [n, 4, 2]), w, T(F32, [k, 8])) == 0
+    # GET_ROWS: 2-D ids with strides, their rows into a 3-D dst
+    ids2 = T(I32, [3, 2], nb=[8, 24, 48, 48])
+    assert a.supports_op(a.OP_GET_ROWS, T(F32, [k, 3, 2]), w, ids2) == 1
+    assert a.supports_op(a.OP_GET_ROWS, T(F16, [k, 3, 2], nb=[2, 2 * k + 256, 6 * k + 768, 0]), w, ids2) == 1
+    assert a.supports_op(a.OP_GET_ROWS, T(F32, [k, 6]), w, ids2) == 0                    # dst shape
+    assert a.supports_op(a.OP_GET_ROWS, T(F32, [k, 3, 2]), w, T(I32, [3, 2], nb=[2, 6, 12, 12])) == 0
+    assert a.supports_op(a.OP_GET_ROWS, T(F32, [k, 3, 2], nb=[4, 2 * k, 12 * k, 24 * k]), w, ids2) == 0
+    assert a.supports_op(a.OP_GET_ROWS, T(F32, [k, 3, 2]), T(Q4, [k, n], False), ids2) == 0   # strided records
+
+
+def test_nd_entries_and_group_sizing_host_checks():
+    """exl3_hip_mul_mat_nd / _get_rows_nd refuse what their predicates refuse before any
+    device work; the group workspace covers the per-matrix GEMM calls of a group."""
+    import ctypes
+    import conftest
+    a = conftest.load_amd()
+    L, T = a.lib(), a.TensorInfo.of
+    k, n = 2048, 6144
+    x, y = T(a.GGML_F32, [k, 4]), T(a.GGML_F32, [n, 4])
+    R, X, Y = 0x100000, 0x200000, 0x300000
+    assert L.exl3_hip_mul_mat_nd(R, 4, 2, k, n, X, ctypes.byref(T(a.GGML_I32, [k, 4])), Y, ctypes.byref(y),
+                                 None, 0, None) == 1
+    assert L.exl3_hip_mul_mat_nd(R, 4, 2, k, n, X, ctypes.byref(x), Y,
+                                 ctypes.byref(T(a.GGML_F32, [n, 4], nb=[4, 4, 16, 16])), None, 0, None) == 1
+    assert L.exl3_hip_mul_mat_nd(R, 4, 2, k, n, X, ctypes.byref(x), Y, ctypes.byref(T(a.GGML_F32, [n, 2, 2])),
+                                 None, 0, None) == 1
+    assert L.exl3_hip_mul_mat_nd(R, 4, 2, k, n, X, ctypes.byref(x), Y, ctypes.byref(y), 0x400000,
+                                 L.exl3_hip_mul_mat_workspace_bytes(k, n, 4) - 1, None) == 3
+    assert L.exl3_hip_mul_mat_nd(R, 4, 2, k, n, X, None, Y, ctypes.byref(y), None, 0, None) == 1
+    ids = T(a.GGML_I32, [5])
+    assert L.exl3_hip_get_rows_nd(R, 4, 2, k, n, X, ctypes.byref(ids), Y,
+                                  ctypes.byref(T(a.GGML_F32, [k, 4])), None, None) == 1
+    assert L.exl3_hip_get_rows_nd(R, 4, 2, k, n, X, ctypes.byref(T(a.GGML_I32, [0])), Y,
+                                  ctypes.byref(T(a.GGML_F32, [k, 0])), None, None) == 0   # no ids: no-op
+    # group sizing: gate/up k = 2048, n = 8192 each, at 513 and 520 rows; the GEMM path runs one
+    # exl3_hip_mul_mat per matrix, whose split partials may exceed the total width's
+    for rows in (513, 520, 33, 8):
+        g = a.group_workspace_bytes(2048, [8192, 8192], rows)
+        assert g >= L.exl3_hip_mul_mat_workspace_bytes(2048, 8192, rows), rows
+        assert g >= L.exl3_hip_mul_mat_workspace_bytes(2048, 16384, rows), rows
+    g = a.group_workspace_bytes(4096, [128, 4608], 33)
+    assert g >= L.exl3_hip_mul_mat_workspace_bytes(4096, 128, 33)
+    assert a.group_workspace_bytes(4096, [128, 4608, 128, 128, 128], 1) == 0   # more than 4 matrices

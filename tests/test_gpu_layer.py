@@ -269,6 +269,26 @@ def test_group_matches_single_layers(amd, oracle, rows):
     assert L.exl3_hip_mul_mat_group(None, 1, 4, 2, 2048, None, 1, 1, 2048, 1, None, 0, None) == 1
 
 
+@pytest.mark.parametrize("rows", [520, 33])
+def test_group_workspace_of_documented_size(amd, rows):
+    """gate/up (k = 2048, n = 8192 each) at rows where the group runs one exl3_hip_mul_mat
+    per matrix, whose split partials need more than the total width's plan: a caller
+    workspace of exactly exl3_hip_mul_mat_group_workspace_bytes is accepted, and each
+    output equals exl3_hip_mul_mat's bit for bit"""
+    import torch
+    k, n, bits = 2048, 8192, 4
+    print(f"  group workspace rows={rows}", flush=True)
+    recs = [dev(make_layer(760 + i, k, n, bits)) for i in range(2)]
+    x = torch.from_numpy(synth.activations(761, rows, k)).cuda()
+    nbytes = amd.group_workspace_bytes(k, [n, n], rows)
+    assert nbytes >= amd.lib().exl3_hip_mul_mat_workspace_bytes(k, n, rows)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    amd.workspace_init(ws)
+    ys = amd.mul_mat_group([(r, n) for r in recs], bits, k, x, workspace=ws)
+    for r, y in zip(recs, ys):
+        assert torch.equal(y, amd.mul_mat(r, bits, k, n, x))
+
+
 def test_concurrent_streams(amd):
     """Calls interleaved on two streams (default priority) at once: with internal
     workspaces (one per device and stream) and with a caller workspace per stream,

@@ -96,11 +96,48 @@ int exl3_hip_supports_mul_mat(unsigned bits, unsigned codebook, size_t k, size_t
 
 // patches/llama-exl3.patch:69-97: the supports_op rules for ops that touch an
 // EXL3 tensor, on plain tensor descriptions; plus the limits of this library's
-// kernels (exl3_hip_supports_mul_mat's dimensions, F32/F16 outputs).
+// kernels (exl3_hip_supports_mul_mat's dimensions, F32/F16 outputs) and the
+// views exl3_hip_mul_mat_nd / exl3_hip_get_rows_nd can address.
 static bool is_exl3(const exl3_tensor_info *t) { return t && (t->type >= 43 && t->type <= 45); }
 static bool is_2d_groups(const exl3_tensor_info *t) {
     return t->ne[0] > 0 && t->ne[1] > 0 && t->ne[0] % 128 == 0 && t->ne[1] % 128 == 0 && t->ne[2] == 1 &&
            t->ne[3] == 1;
+}
+
+// A ggml view as rows (src/exl3-ggml.cpp:11-17): row r = i1 + ne[1] (i2 + ne[2] i3)
+// starts at byte i1 nb[1] + i2 nb[2] + i3 nb[3].  Valid when dimension 0 is dense
+// (nb[0] = es), every row stride is a multiple of es, and the row count is in
+// range; with `disjoint` no two rows may share a byte (the view is written).
+static bool rows_view_ok(const exl3_tensor_info *t, size_t es, int64_t row_len, bool disjoint) {
+    if (t->ne[0] != row_len || t->nb[0] != es) return false;
+    size_t rows = 1;
+    for (int d = 1; d < 4; ++d) {
+        if (t->ne[d] < 0 || (size_t)t->ne[d] > kMaxRows || t->nb[d] % es) return false;
+        rows *= (size_t)t->ne[d];
+        if (rows > kMaxRows) return false;
+    }
+    if (!disjoint) return true;
+    // the dimensions that step (ne > 1) in stride order: each stride must clear
+    // the extent of the rows below it (a sufficient condition for no overlap)
+    std::pair<size_t, size_t> dims[3];
+    int c = 0;
+    for (int d = 1; d < 4; ++d)
+        if (t->ne[d] > 1) dims[c++] = std::make_pair(t->nb[d], (size_t)t->ne[d]);
+    std::sort(dims, dims + c);
+    size_t extent = (size_t)row_len * es;
+    for (int i = 0; i < c; ++i) {
+        if (dims[i].first < extent) return false;
+        if (dims[i].first > SIZE_MAX / dims[i].second) return false;  // an address range no device has
+        extent = dims[i].first * dims[i].second;
+    }
+    return true;
+}
+static size_t view_rows(const exl3_tensor_info *t) { return (size_t)t->ne[1] * (size_t)t->ne[2] * (size_t)t->ne[3]; }
+static bool dtype_of(unsigned ggml_type, exl3_dtype *dt) {
+    if (ggml_type == EXL3_GGML_TYPE_F32) *dt = EXL3_F32;
+    else if (ggml_type == EXL3_GGML_TYPE_F16) *dt = EXL3_F16;
+    else return false;
+    return true;
 }
 
 int exl3_hip_supports_op(exl3_op op, const exl3_tensor_info *dst, const exl3_tensor_info *src0,
@@ -116,20 +153,31 @@ int exl3_hip_supports_op(exl3_op op, const exl3_tensor_info *dst, const exl3_ten
     case EXL3_OP_MUL_MAT: {
         if (!is_exl3(src0)) return -1;
         if (!src1 || !is_2d_groups(src0) || !src0->contiguous) return 0;
-        if (src1->type != EXL3_GGML_TYPE_F32 && src1->type != EXL3_GGML_TYPE_F16) return 0;
-        if (dst->type != EXL3_GGML_TYPE_F32) return 0;
-        const int64_t rows = src1->ne[1] * src1->ne[2] * src1->ne[3];
-        if (src1->ne[0] != src0->ne[0] || rows < 1) return 0;
+        exl3_dtype xt;
+        if (!dtype_of(src1->type, &xt) || dst->type != EXL3_GGML_TYPE_F32) return 0;
+        // dst = [ne01, ne11, ne12, ne13]; every row of src1 and dst addressable
+        if (dst->ne[0] != src0->ne[1] || dst->ne[1] != src1->ne[1] || dst->ne[2] != src1->ne[2] ||
+            dst->ne[3] != src1->ne[3])
+            return 0;
+        if (!rows_view_ok(src1, dtype_size(xt), src0->ne[0], false) || !rows_view_ok(dst, 4, src0->ne[1], true))
+            return 0;
         return exl3_hip_supports_mul_mat(exl3_type_bits(src0->type), EXL3_CB_MUL1, (size_t)src0->ne[0],
-                                         (size_t)src0->ne[1], (size_t)rows,
-                                         src1->type == EXL3_GGML_TYPE_F16 ? EXL3_F16 : EXL3_F32, EXL3_F32);
+                                         (size_t)src0->ne[1], view_rows(src1), xt, EXL3_F32);
     }
-    case EXL3_OP_GET_ROWS:
+    case EXL3_OP_GET_ROWS: {
         if (!is_exl3(src0)) return -1;
-        if (!src1 || !is_2d_groups(src0) || src1->type != EXL3_GGML_TYPE_I32) return 0;
-        if (dst->type != EXL3_GGML_TYPE_F32 && dst->type != EXL3_GGML_TYPE_F16) return 0;
+        if (!src1 || !is_2d_groups(src0) || !src0->contiguous || src1->type != EXL3_GGML_TYPE_I32) return 0;
+        exl3_dtype ot;
+        if (!dtype_of(dst->type, &ot)) return 0;
+        // ids [ne10, ne11, ne12] (ne13 = 1) -> dst [ne00, ne10, ne11, ne12]
+        if (src1->ne[3] != 1 || src1->nb[0] % 4 || src1->nb[1] % 4 || src1->nb[2] % 4) return 0;
+        if (dst->ne[0] != src0->ne[0] || dst->ne[1] != src1->ne[0] || dst->ne[2] != src1->ne[1] ||
+            dst->ne[3] != src1->ne[2])
+            return 0;
+        if (!rows_view_ok(dst, dtype_size(ot), src0->ne[0], true)) return 0;
         return exl3_hip_supports_mul_mat(exl3_type_bits(src0->type), EXL3_CB_MUL1, (size_t)src0->ne[0],
                                          (size_t)src0->ne[1], 1, EXL3_F32, EXL3_F32);
+    }
     }
     return 0;
 }
@@ -159,8 +207,44 @@ size_t exl3_hip_mul_mat_workspace_bytes(size_t k, size_t n, size_t rows) {
 }
 
 exl3_status exl3_hip_workspace_init(void *workspace, size_t workspace_bytes, hipStream_t stream) {
-    if (!workspace || !aligned(workspace, 256)) return EXL3_INVAL_PARAMS;
+    if (!workspace) {  // the internal workspace of (current device, stream), if there is one
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return EXL3_HIP_ERROR;
+        std::lock_guard<std::mutex> lock(g_ws_mutex);
+        const auto it = g_ws.find(std::make_pair(dev, stream));
+        if (it == g_ws.end() || !it->second.ptr) return EXL3_OK;
+        return from_hip(exl3k::launch_zero(it->second.ptr, it->second.bytes, stream));
+    }
+    if (!aligned(workspace, 256)) return EXL3_INVAL_PARAMS;
     return from_hip(exl3k::launch_zero(workspace, workspace_bytes, stream));
+}
+
+exl3_status exl3_hip_workspace_status(const void *workspace, size_t workspace_bytes, int *faulted,
+                                      hipStream_t stream) {
+    if (!faulted) return EXL3_INVAL_PARAMS;
+    *faulted = 0;
+    const uint8_t *ws = (const uint8_t *)workspace;
+    if (!ws) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return EXL3_HIP_ERROR;
+        std::lock_guard<std::mutex> lock(g_ws_mutex);
+        const auto it = g_ws.find(std::make_pair(dev, stream));
+        if (it == g_ws.end() || !it->second.ptr) return EXL3_OK;  // never used: nothing can have failed
+        ws = (const uint8_t *)it->second.ptr;
+    } else if (!aligned(ws, 256) || workspace_bytes < exl3k::kSharedPrefixBytes) {
+        return EXL3_INVAL_PARAMS;
+    }
+    uint32_t word = 0;
+    if (hipMemcpyAsync(&word, ws + exl3k::kStatusOffset, sizeof(word), hipMemcpyDeviceToHost, stream) != hipSuccess ||
+        hipStreamSynchronize(stream) != hipSuccess)
+        return EXL3_HIP_ERROR;
+    *faulted = word != 0u;
+    return EXL3_OK;
+}
+
+exl3_status exl3_hip_test_exchange_fault(int spin_limit, int drop_split) {
+    exl3k::set_exchange_fault(spin_limit, drop_split);
+    return EXL3_OK;
 }
 
 static exl3_status mul_mat_impl(const void *records, unsigned bits, unsigned codebook, size_t k, size_t n,
@@ -228,6 +312,19 @@ exl3_status exl3_hip_mul_mat_group(const exl3_matrix_desc *mats, size_t count, u
         n_total += m.n;
     }
     if (!x || !aligned(x, dtype_size(xt)) || x_row_stride < k || n_total > kMaxDim) return EXL3_INVAL_PARAMS;
+    // the workspace is checked (or the internal one grown) before anything is
+    // enqueued, for whichever of the two paths below the call takes
+    size_t ns[exl3k::kGemvMaxTargets];
+    for (size_t i = 0; i < count; ++i) ns[i] = mats[i].n;
+    const size_t need = exl3_hip_mul_mat_group_workspace_bytes(k, ns, count, rows);
+    if (workspace) {
+        if (!aligned(workspace, 256)) return EXL3_INVAL_PARAMS;
+        if (workspace_bytes < need) return EXL3_WORKSPACE_TOO_SMALL;
+    } else {
+        const exl3_status st = internal_workspace(need, stream, &workspace);
+        if (st != EXL3_OK) return st;
+        workspace_bytes = need;
+    }
     // GEMM (or, for one matrix above the single-matrix GEMV rows, whichever
     // exl3_hip_mul_mat picks): one call per matrix, each a full-size launch
     if (!exl3k::gemv_serves(k, n_total, rows) || (count == 1 && rows > (size_t)exl3k::kGemvSingleMaxRows)) {
@@ -238,14 +335,6 @@ exl3_status exl3_hip_mul_mat_group(const exl3_matrix_desc *mats, size_t count, u
             if (st != EXL3_OK) return st;
         }
         return EXL3_OK;
-    }
-    const size_t need = exl3_hip_mul_mat_workspace_bytes(k, n_total, rows);
-    if (workspace) {
-        if (!aligned(workspace, 256)) return EXL3_INVAL_PARAMS;
-        if (workspace_bytes < need) return EXL3_WORKSPACE_TOO_SMALL;
-    } else {
-        const exl3_status st = internal_workspace(need, stream, &workspace);
-        if (st != EXL3_OK) return st;
     }
     exl3k::GemvTargets tg{};
     int nb_end = 0;
@@ -259,6 +348,108 @@ exl3_status exl3_hip_mul_mat_group(const exl3_matrix_desc *mats, size_t count, u
     tg.count = (int)count;
     return from_hip(exl3k::launch_gemv_targets(tg, (int)bits, (int)codebook, x, xt == EXL3_F16, rows, x_row_stride,
                                                yt == EXL3_F16, workspace, exl3k::gemv_plan(k, n_total, rows), stream));
+}
+
+size_t exl3_hip_mul_mat_group_workspace_bytes(size_t k, const size_t *n, size_t count, size_t rows) {
+    if (!n || count < 1 || count > (size_t)exl3k::kGemvMaxTargets) return 0;
+    size_t n_total = 0, need = 0;
+    for (size_t i = 0; i < count; ++i) {
+        const size_t b = exl3_hip_mul_mat_workspace_bytes(k, n[i], rows);
+        if (!b) return 0;
+        need = std::max(need, b);  // the per-matrix calls of the GEMM path
+        n_total += n[i];
+    }
+    if (n_total > kMaxDim) return 0;
+    return std::max(need, exl3_hip_mul_mat_workspace_bytes(k, n_total, rows));  // the one GEMV launch
+}
+
+exl3_status exl3_hip_mul_mat_nd(const void *records, unsigned bits, unsigned codebook, size_t k, size_t n,
+                                const void *x, const exl3_tensor_info *x_info, void *y,
+                                const exl3_tensor_info *y_info, void *workspace, size_t workspace_bytes,
+                                hipStream_t stream) {
+    exl3_dtype xt, yt;
+    if (!x_info || !y_info || !dtype_of(x_info->type, &xt) || !dtype_of(y_info->type, &yt)) return EXL3_INVAL_PARAMS;
+    const size_t xes = dtype_size(xt), yes = dtype_size(yt);
+    if (!valid_matrix(k, n, 128)) return EXL3_INVAL_PARAMS;
+    if (!rows_view_ok(x_info, xes, (int64_t)k, false) || !rows_view_ok(y_info, yes, (int64_t)n, true))
+        return EXL3_INVAL_PARAMS;
+    for (int d = 1; d < 4; ++d)
+        if (x_info->ne[d] != y_info->ne[d]) return EXL3_INVAL_PARAMS;
+    const size_t rows = view_rows(x_info);
+    if (!exl3_hip_supports_mul_mat(bits, codebook, k, n, rows, xt, yt) || !records || !x || !y)
+        return EXL3_INVAL_PARAMS;
+    const size_t need = exl3_hip_mul_mat_workspace_bytes(k, n, rows);  // every call below needs at most this
+    if (workspace) {
+        if (!aligned(workspace, 256)) return EXL3_INVAL_PARAMS;
+        if (workspace_bytes < need) return EXL3_WORKSPACE_TOO_SMALL;
+    } else {
+        const exl3_status st = internal_workspace(need, stream, &workspace);
+        if (st != EXL3_OK) return st;
+        workspace_bytes = need;
+    }
+    // Row dimensions 1, 2, 3 in order join one run while both views step through
+    // them with one row stride (a run's stride at least a row, as exl3_hip_mul_mat
+    // takes it); the run is one call, the dimensions from `outer` on loop.
+    size_t run = 1, xs = k, ys = n;  // rows of the run, its strides in elements
+    int outer = 4;
+    for (int d = 1; d < 4 && outer == 4; ++d) {
+        const size_t ne = (size_t)x_info->ne[d], xnb = x_info->nb[d] / xes, ynb = y_info->nb[d] / yes;
+        if (ne == 1) continue;
+        if (run == 1 && xnb >= k && ynb >= n) {
+            xs = xnb;
+            ys = ynb;
+            run = ne;
+        } else if (run > 1 && xnb == xs * run && ynb == ys * run) {
+            run *= ne;
+        } else {
+            outer = d;
+        }
+    }
+    size_t count[4] = {1, 1, 1, 1};
+    for (int d = outer; d < 4; ++d) count[d] = (size_t)x_info->ne[d];
+    for (size_t i3 = 0; i3 < count[3]; ++i3)
+        for (size_t i2 = 0; i2 < count[2]; ++i2)
+            for (size_t i1 = 0; i1 < count[1]; ++i1) {
+                const size_t xo = i1 * x_info->nb[1] + i2 * x_info->nb[2] + i3 * x_info->nb[3];
+                const size_t yo = i1 * y_info->nb[1] + i2 * y_info->nb[2] + i3 * y_info->nb[3];
+                const exl3_status st = mul_mat_impl(records, bits, codebook, k, n, (const uint8_t *)x + xo, xt, run,
+                                                    xs, nullptr, 0, (uint8_t *)y + yo, yt, ys, workspace,
+                                                    workspace_bytes, stream);
+                if (st != EXL3_OK) return st;
+            }
+    return EXL3_OK;
+}
+
+exl3_status exl3_hip_get_rows_nd(const void *records, unsigned bits, unsigned codebook, size_t k, size_t n,
+                                 const int32_t *ids, const exl3_tensor_info *ids_info, void *out,
+                                 const exl3_tensor_info *out_info, int *bad_ids, hipStream_t stream) {
+    exl3_dtype ot;
+    if (!ids_info || !out_info || !dtype_of(out_info->type, &ot)) return EXL3_INVAL_PARAMS;
+    if (!valid_rate(bits, codebook) || !valid_matrix(k, n, 128)) return EXL3_INVAL_PARAMS;
+    if (ids_info->type != EXL3_GGML_TYPE_I32 || ids_info->ne[3] != 1) return EXL3_INVAL_PARAMS;
+    for (int d = 0; d < 3; ++d)
+        if (ids_info->ne[d] < 0 || ids_info->nb[d] % 4 || out_info->ne[d + 1] != ids_info->ne[d])
+            return EXL3_INVAL_PARAMS;
+    const size_t es = dtype_size(ot);
+    if (!rows_view_ok(out_info, es, (int64_t)k, true)) return EXL3_INVAL_PARAMS;
+    const size_t per = (size_t)ids_info->ne[0];
+    if (!view_rows(out_info)) return EXL3_OK;
+    if (!records || !ids || !out || !aligned(records, 16) || !aligned(ids, 4) || !aligned(out, es) ||
+        (bad_ids && !aligned(bad_ids, 4)))
+        return EXL3_INVAL_PARAMS;
+    // one launch per (i1, i2) of the ids: ne[0] ids at stride nb[0], their rows at
+    // stride out nb[1] (any stride serves a single row)
+    const size_t out_stride = per > 1 ? out_info->nb[1] / es : k;
+    for (int64_t i2 = 0; i2 < ids_info->ne[2]; ++i2)
+        for (int64_t i1 = 0; i1 < ids_info->ne[1]; ++i1) {
+            const int32_t *id = (const int32_t *)((const uint8_t *)ids + i1 * ids_info->nb[1] + i2 * ids_info->nb[2]);
+            void *o = (uint8_t *)out + i1 * out_info->nb[2] + i2 * out_info->nb[3];
+            const hipError_t e = exl3k::launch_get_rows(records, (int)bits, (int)codebook, k, n, id,
+                                                        ids_info->nb[0] / 4, per, o, ot == EXL3_F16, out_stride,
+                                                        bad_ids, stream);
+            if (e != hipSuccess) return EXL3_HIP_ERROR;
+        }
+    return EXL3_OK;
 }
 
 exl3_status exl3_hip_decode_batch(const exl3_decode_desc *descs, size_t count, exl3_layout layout,
@@ -342,7 +533,7 @@ exl3_status exl3_hip_get_rows(const void *records, unsigned bits, unsigned codeb
     if (count > 0x7fffffffu || !records || !ids || !out || !aligned(records, 16) || !aligned(ids, 4) ||
         !aligned(out, dtype_size(ot)) || out_row_stride < k || (bad_ids && !aligned(bad_ids, 4)))
         return EXL3_INVAL_PARAMS;
-    return from_hip(exl3k::launch_get_rows(records, (int)bits, (int)codebook, k, n, ids, count, out, ot == EXL3_F16,
+    return from_hip(exl3k::launch_get_rows(records, (int)bits, (int)codebook, k, n, ids, 1, count, out, ot == EXL3_F16,
                                            out_row_stride, bad_ids, stream));
 }
 

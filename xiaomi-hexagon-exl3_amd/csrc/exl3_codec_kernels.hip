@@ -297,14 +297,15 @@ hipError_t launch_reconstruct(const void *src, int rl, const uint16_t *su, const
 // An id outside [0, n) writes a NaN row and sets *bad_ids (if given) to 1.
 template <int K, int CB>
 __global__ __launch_bounds__(256) void get_rows_kernel(const uint8_t *__restrict__ records, size_t k, size_t n,
-                                                       const int32_t *__restrict__ ids, void *__restrict__ out,
-                                                       int out_f16, size_t out_stride, int *__restrict__ bad_ids) {
+                                                       const int32_t *__restrict__ ids, size_t ids_stride,
+                                                       void *__restrict__ out, int out_f16, size_t out_stride,
+                                                       int *__restrict__ bad_ids) {
     constexpr int P = 129;
     __shared__ float blk[128 * P];
     __shared__ float colv[128];
     const int tid = threadIdx.x;
     const size_t r = blockIdx.x, kb = blockIdx.y;
-    const int32_t id = ids[r];
+    const int32_t id = ids[r * ids_stride];
     const size_t o = r * out_stride + kb * 128;
     if (id < 0 || (size_t)id >= n) {
         if (tid < 128) {
@@ -374,29 +375,34 @@ __global__ __launch_bounds__(256) void get_rows_kernel(const uint8_t *__restrict
 }
 
 template <int K>
-static hipError_t launch_get_rows_k(const void *records, int cb, size_t k, size_t n, const int32_t *ids, size_t count,
-                                    void *out, int out_f16, size_t out_stride, int *bad_ids, hipStream_t stream) {
+static hipError_t launch_get_rows_k(const void *records, int cb, size_t k, size_t n, const int32_t *ids,
+                                    size_t ids_stride, size_t count, void *out, int out_f16, size_t out_stride,
+                                    int *bad_ids, hipStream_t stream) {
     const dim3 grid((unsigned)count, (unsigned)(k / 128)), block(256);
     const uint8_t *rec = (const uint8_t *)records;
     switch (cb) {
-    case 0: get_rows_kernel<K, 0><<<grid, block, 0, stream>>>(rec, k, n, ids, out, out_f16, out_stride, bad_ids); break;
-    case 1: get_rows_kernel<K, 1><<<grid, block, 0, stream>>>(rec, k, n, ids, out, out_f16, out_stride, bad_ids); break;
-    default: get_rows_kernel<K, 2><<<grid, block, 0, stream>>>(rec, k, n, ids, out, out_f16, out_stride, bad_ids); break;
+    case 0: get_rows_kernel<K, 0><<<grid, block, 0, stream>>>(rec, k, n, ids, ids_stride, out, out_f16, out_stride,
+                                                                 bad_ids); break;
+    case 1: get_rows_kernel<K, 1><<<grid, block, 0, stream>>>(rec, k, n, ids, ids_stride, out, out_f16, out_stride,
+                                                                 bad_ids); break;
+    default: get_rows_kernel<K, 2><<<grid, block, 0, stream>>>(rec, k, n, ids, ids_stride, out, out_f16, out_stride,
+                                                                 bad_ids); break;
     }
     return hipGetLastError();
 }
 
-hipError_t launch_get_rows(const void *records, int bits, int cb, size_t k, size_t n, const int32_t *ids, size_t count,
-                           void *out, int out_f16, size_t out_stride, int *bad_ids, hipStream_t stream) {
+hipError_t launch_get_rows(const void *records, int bits, int cb, size_t k, size_t n, const int32_t *ids,
+                           size_t ids_stride, size_t count, void *out, int out_f16, size_t out_stride, int *bad_ids,
+                           hipStream_t stream) {
     switch (bits) {
-    case 1: return launch_get_rows_k<1>(records, cb, k, n, ids, count, out, out_f16, out_stride, bad_ids, stream);
-    case 2: return launch_get_rows_k<2>(records, cb, k, n, ids, count, out, out_f16, out_stride, bad_ids, stream);
-    case 3: return launch_get_rows_k<3>(records, cb, k, n, ids, count, out, out_f16, out_stride, bad_ids, stream);
-    case 4: return launch_get_rows_k<4>(records, cb, k, n, ids, count, out, out_f16, out_stride, bad_ids, stream);
-    case 5: return launch_get_rows_k<5>(records, cb, k, n, ids, count, out, out_f16, out_stride, bad_ids, stream);
-    case 6: return launch_get_rows_k<6>(records, cb, k, n, ids, count, out, out_f16, out_stride, bad_ids, stream);
-    case 7: return launch_get_rows_k<7>(records, cb, k, n, ids, count, out, out_f16, out_stride, bad_ids, stream);
-    default: return launch_get_rows_k<8>(records, cb, k, n, ids, count, out, out_f16, out_stride, bad_ids, stream);
+    case 1: return launch_get_rows_k<1>(records, cb, k, n, ids, ids_stride, count, out, out_f16, out_stride, bad_ids, stream);
+    case 2: return launch_get_rows_k<2>(records, cb, k, n, ids, ids_stride, count, out, out_f16, out_stride, bad_ids, stream);
+    case 3: return launch_get_rows_k<3>(records, cb, k, n, ids, ids_stride, count, out, out_f16, out_stride, bad_ids, stream);
+    case 4: return launch_get_rows_k<4>(records, cb, k, n, ids, ids_stride, count, out, out_f16, out_stride, bad_ids, stream);
+    case 5: return launch_get_rows_k<5>(records, cb, k, n, ids, ids_stride, count, out, out_f16, out_stride, bad_ids, stream);
+    case 6: return launch_get_rows_k<6>(records, cb, k, n, ids, ids_stride, count, out, out_f16, out_stride, bad_ids, stream);
+    case 7: return launch_get_rows_k<7>(records, cb, k, n, ids, ids_stride, count, out, out_f16, out_stride, bad_ids, stream);
+    default: return launch_get_rows_k<8>(records, cb, k, n, ids, ids_stride, count, out, out_f16, out_stride, bad_ids, stream);
     }
 }
 

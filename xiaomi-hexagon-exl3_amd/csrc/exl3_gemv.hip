@@ -8,6 +8,7 @@
 
 #include <stdint.h>
 
+#include <atomic>
 #include <type_traits>
 
 #include "exl3_kernel_common.hpp"
@@ -65,7 +66,7 @@ template <int K, int CB, int MODE>
 __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void gemv_kernel(
     GemvTargets tg, int kbs, int splits, int kq, int kr, const void *__restrict__ x, int x_f16, size_t x_stride,
     int rows, const uint8_t *__restrict__ dummy, uint32_t *__restrict__ partials, int y_f16,
-    const uint8_t *__restrict__ xpre) {
+    const uint8_t *__restrict__ xpre, uint32_t *__restrict__ status, int spin_limit, int drop_split) {
     constexpr bool TWO = MODE >= 1, HILO = MODE <= 1;
     constexpr int W = kGemvWaves;
     constexpr int P = W / 4;  // waves per column pair
@@ -423,6 +424,7 @@ __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu
     if (splits > 1) {
         uint32_t *all = partials + (size_t)nb * splits * (size_t)nval;
         if (s != splits - 1) {  // hand the partial over and end
+            if (s == drop_split) return;  // failure injection (tests only): this partial never arrives
             uint32_t *mine = all + (size_t)s * nval;
 #pragma unroll
             for (int i = 0; i < PER; ++i) {
@@ -435,14 +437,20 @@ __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu
         // the splits in split order, its own partial (from LDS) last, a batch of
         // splits' loads in flight together, straight into the registers of the
         // output transform.  A word still empty is read again (with the rest of
-        // its batch) until it is full.
+        // its batch) until it is full, or until the wave's budget of polls runs
+        // out or another wave of the workgroup has given up (`gave_up`).  A
+        // workspace whose status word is set gives NaN without waiting.
+        int *gave_up = (int *)(own + nval);  // LDS, after the workgroup partial
+        const uint32_t poisoned = load_exchange(status);
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int t = tid + i * NT;
             if (t < nval) own[t] = psum[i];
         }
+        if (tid == 0) *gave_up = poisoned != 0u;
         __syncthreads();
         const int nsp = splits - 1;  // splits in the exchange
+        int budget = spin_limit;
         for (int rr = wave; rr < rows; rr += W) {
             constexpr int B = 16;
             float a0 = 0.f, a1 = 0.f;
@@ -465,7 +473,12 @@ __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu
                         if (base + jb < nsp) z |= (v0[jb] == 0u) | (v1[jb] == 0u);
                     return z != 0;
                 };
-                for (int pass = 0; __builtin_amdgcn_ballot_w64(any_empty()) && pass < kExchangeSpinLimit; ++pass) {
+                while (__builtin_amdgcn_ballot_w64(any_empty())) {
+                    if (__hip_atomic_load(gave_up, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) break;
+                    if (--budget < 0) {
+                        __hip_atomic_store(gave_up, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                        break;
+                    }
                     __builtin_amdgcn_s_sleep(2);
                     // the addresses are formed again in every pass (the empty asm hides
                     // that they repeat), so they hold no registers across the loop
@@ -476,14 +489,16 @@ __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu
 #pragma unroll
                 for (int jb = 0; jb < B; ++jb)
                     if (base + jb < nsp) {  // a word that never filled: a loud result, not a hang
-                        a0 += v0[jb] ? exchange_value(v0[jb]) : __builtin_nanf("");
-                        a1 += v1[jb] ? exchange_value(v1[jb]) : __builtin_nanf("");
+                        a0 += v0[jb] && !poisoned ? exchange_value(v0[jb]) : __builtin_nanf("");
+                        a1 += v1[jb] && !poisoned ? exchange_value(v1[jb]) : __builtin_nanf("");
                     }
             }
             finish_row(rr, a0 + own[rr * 128 + lane], a1 + own[rr * 128 + lane + 64]);
         }
-        // every word has been read: empty them for the next call
+        // every word has been read: empty them for the next call; after a give-up
+        // a partial may still arrive, so the status word marks the workspace
         __syncthreads();
+        if (tid == 0 && *gave_up && !poisoned) __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         for (int t = tid; t < nsp * nval; t += NT) clear_exchange(all + t);
         return;
     }
@@ -537,10 +552,10 @@ __global__ __launch_bounds__(256) void gemv_xprep_kernel(GemvTargets tg, int bit
 static size_t gemv_frag_bytes_per_kb(size_t rows) { return (rows > 16 ? 256 : 512) * rows; }
 
 // LDS bytes of a GEMV workgroup: its B fragments, reused after the main loop for
-// the P partials and the output rows
+// the P partials, the output rows and the summing workgroup's give-up flag
 static size_t gemv_lds_bytes(int nkb_max, size_t rows) {
     const size_t frag = (size_t)nkb_max * gemv_frag_bytes_per_kb(rows);
-    const size_t red = (size_t)(kGemvWaves / 4 + 1) * rows * 128 * 4;
+    const size_t red = (size_t)(kGemvWaves / 4 + 1) * rows * 128 * 4 + 16;
     return ((frag > red ? frag : red) + 15) & ~(size_t)15;
 }
 
@@ -583,6 +598,13 @@ bool gemv_serves(size_t k, size_t n, size_t rows) {
     return rows >= 1 && rows <= (size_t)kGemvMaxRows && gemv_plan(k, n, rows).fits;
 }
 
+static std::atomic<int> g_fault_spin_limit{0}, g_fault_drop_split{-1};
+
+void set_exchange_fault(int spin_limit, int drop_split) {
+    g_fault_spin_limit.store(spin_limit > 0 ? spin_limit : 0, std::memory_order_relaxed);
+    g_fault_drop_split.store(drop_split >= 0 ? drop_split : -1, std::memory_order_relaxed);
+}
+
 template <int K, int CB>
 static hipError_t launch_gemv_kc(const GemvTargets &tg, const void *x, int x_f16, size_t rows, size_t x_stride,
                                  int y_f16, uint8_t *ws, const GemvPlan &p, hipStream_t stream) {
@@ -592,19 +614,25 @@ static hipError_t launch_gemv_kc(const GemvTargets &tg, const void *x, int x_f16
     const dim3 grid((unsigned)p.nbs, (unsigned)p.splits), block(kGemvWaves * 64);
     const int kq = p.kbs / p.splits, kr = p.kbs % p.splits;
     uint32_t *part = (uint32_t *)(ws + p.partials_off);
+    uint32_t *status = (uint32_t *)(ws + kStatusOffset);
+    const int spin = g_fault_spin_limit.load(std::memory_order_relaxed);
+    const int spin_limit = spin > 0 ? spin : kExchangeSpinLimit;
+    const int drop_split = g_fault_drop_split.load(std::memory_order_relaxed);
     if (rows > 16) {
         uint16_t *xp = (uint16_t *)(ws + p.xpre_off);
         gemv_xprep_kernel<<<dim3((unsigned)((rows + 3) / 4), (unsigned)p.kbs, (unsigned)tg.count), dim3(256), 0,
                             stream>>>(tg, K, x, x_f16, x_stride, (int)rows, p.kbs, xp);
         gemv_kernel<K, CB, 2><<<grid, block, lds, stream>>>(tg, p.kbs, p.splits, kq, kr, x, x_f16, x_stride,
                                                             (int)rows, ws + p.dummy_off, part, y_f16,
-                                                            (const uint8_t *)xp);
+                                                            (const uint8_t *)xp, status, spin_limit, drop_split);
     } else if (rows > 8) {
         gemv_kernel<K, CB, 1><<<grid, block, lds, stream>>>(tg, p.kbs, p.splits, kq, kr, x, x_f16, x_stride,
-                                                            (int)rows, ws + p.dummy_off, part, y_f16, nullptr);
+                                                            (int)rows, ws + p.dummy_off, part, y_f16, nullptr,
+                                                            status, spin_limit, drop_split);
     } else {
         gemv_kernel<K, CB, 0><<<grid, block, lds, stream>>>(tg, p.kbs, p.splits, kq, kr, x, x_f16, x_stride,
-                                                            (int)rows, ws + p.dummy_off, part, y_f16, nullptr);
+                                                            (int)rows, ws + p.dummy_off, part, y_f16, nullptr,
+                                                            status, spin_limit, drop_split);
     }
     return hipGetLastError();
 }

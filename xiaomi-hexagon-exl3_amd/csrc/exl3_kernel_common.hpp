@@ -46,8 +46,12 @@ __device__ __forceinline__ float mul_rn_f32(float a, float b) {
 // workgroups wait, and only for workgroups that wait for nothing.  The split is
 // the grid's slowest dimension, so the summing workgroups are the grid's last:
 // on every XCD the others are dispatched before any of them and never need a
-// slot that a waiting workgroup holds, and every wait ends.
-constexpr int kExchangeSpinLimit = 1 << 20;
+// slot that a waiting workgroup holds, and every wait ends.  Each wait is also
+// bounded: a wave that has polled kExchangeSpinLimit times, or whose workgroup
+// has already given up, stops waiting; the words still empty count as NaN and
+// the workspace's status word (kStatusOffset) is set, which makes every later
+// call with that workspace NaN until it is zero-filled again.
+constexpr int kExchangeSpinLimit = 1 << 20;  // polls per wave of the summing workgroup before it gives up
 
 // binary32 bits complemented; the one value whose complement is zero (the NaN
 // 0xffffffff) is stored as 1, which reads back as the NaN 0xfffffffe

@@ -31,8 +31,22 @@ constexpr int kGemvWaves = 8;     // waves per GEMV workgroup (a multiple of 4)
 // second kernel sums its split partials.
 constexpr size_t kGemmSplitTiles = 512;
 constexpr size_t kGemvExchangeBytes = (size_t)16 << 20;
-// bytes every workspace starts with: the exchange
-constexpr size_t kSharedPrefixBytes = kGemvExchangeBytes;
+// Right after the exchange: the status word (32 bits, in a 256-byte block).
+// Zero while the exchange can be trusted.  A workgroup that gives up waiting for
+// a split's partial (a bounded wait that ran out) sets it to 1; from then on a
+// partial stored late may sit in the exchange, so every later GEMV call with
+// that workspace writes NaN for every output it sums, without waiting, until
+// the workspace is zero-filled again (exl3_hip_workspace_init).
+constexpr size_t kStatusOffset = kGemvExchangeBytes;
+constexpr size_t kStatusBytes = 256;
+// bytes every workspace starts with: the exchange and the status block
+constexpr size_t kSharedPrefixBytes = kGemvExchangeBytes + kStatusBytes;
+
+// Failure injection for tests of the give-up path (never set by a product
+// caller): spin_limit > 0 replaces the wait budget of the split-K hand-off (in
+// polls per wave); drop_split >= 0 makes that split's workgroups skip storing
+// their partial.  set_exchange_fault(0, -1) restores the defaults.
+void set_exchange_fault(int spin_limit, int drop_split);
 
 // Up to kGemvMaxTargets matrices that share k, the bit rate, the codebook and x,
 // served by one GEMV launch: column groups [nb_end[i-1], nb_end[i]) belong to
@@ -91,8 +105,10 @@ hipError_t launch_decode_batch(const DecodeBatch &batch, int records_layout, int
 hipError_t launch_reconstruct(const void *src, int records_layout, const uint16_t *su, const uint16_t *sv,
                               int bits, int cb, size_t k, size_t n, size_t first, size_t count, uint16_t *out,
                               hipStream_t stream);
-hipError_t launch_get_rows(const void *records, int bits, int cb, size_t k, size_t n, const int32_t *ids, size_t count,
-                           void *out, int out_f16, size_t out_stride, int *bad_ids, hipStream_t stream);
+// ids[i * ids_stride] for i < count (ids_stride in int32 elements, may be 0)
+hipError_t launch_get_rows(const void *records, int bits, int cb, size_t k, size_t n, const int32_t *ids,
+                           size_t ids_stride, size_t count, void *out, int out_f16, size_t out_stride, int *bad_ids,
+                           hipStream_t stream);
 hipError_t launch_codebook(const uint16_t *states, size_t count, int cb, uint16_t *out, hipStream_t stream);
 hipError_t launch_hadamard(float *values, size_t count, hipStream_t stream);
 hipError_t launch_pack_records(const uint16_t *packed, const uint16_t *su, const uint16_t *sv, int bits, size_t k,

@@ -26,7 +26,8 @@ EXPORTS = [
     "exl3_hip_model_embedding", "exl3_hip_model_matrix_count", "exl3_hip_model_matrix", "exl3_hip_model_record_bytes",
     "exl3_hip_model_upload_records", "exl3_hip_iface_matmul_workspace_bytes", "exl3_hip_iface_matmul",
     "exl3_hip_supports_op", "exl3_hip_model_embedding_tables", "exl3_hip_model_embedding_table",
-    "exl3_hip_mul_mat_noalloc",
+    "exl3_hip_mul_mat_noalloc", "exl3_hip_mul_mat_nd", "exl3_hip_get_rows_nd",
+    "exl3_hip_mul_mat_group_workspace_bytes", "exl3_hip_workspace_status", "exl3_hip_test_exchange_fault",
 ]
 
 # ggml op predicates (exl3_hip_supports_op)
@@ -34,14 +35,40 @@ OP_MUL_MAT, OP_MUL_MAT_ID, OP_GET_ROWS, OP_CPY, OP_SET_ROWS = range(5)
 GGML_F32, GGML_F16, GGML_I32 = 0, 1, 26
 
 
+# bytes per ggml block and elements per block of the types used here (ggml's type
+# traits; the EXL3 types 43/44/45 are 128-element blocks of 16 K + 4 bytes)
+GGML_TYPE_BLOCK = {0: (4, 1), 1: (2, 1), 26: (4, 1), 27: (8, 1), 30: (2, 1),
+                   43: (68, 128), 44: (100, 128), 45: (132, 128)}
+
+
 class TensorInfo(ctypes.Structure):
-    """exl3_tensor_info: a ggml tensor's type, ne[4] and contiguity"""
-    _fields_ = [("type", ctypes.c_uint), ("ne", ctypes.c_int64 * 4), ("contiguous", ctypes.c_int)]
+    """exl3_tensor_info: a ggml tensor's type, ne[4], contiguity and nb[4] (byte strides)"""
+    _fields_ = [("type", ctypes.c_uint), ("ne", ctypes.c_int64 * 4), ("contiguous", ctypes.c_int),
+                ("nb", ctypes.c_size_t * 4)]
 
     @classmethod
-    def of(cls, type_, ne, contiguous=True):
+    def of(cls, type_, ne, contiguous=True, nb=None):
+        """ne (padded with 1s to four dimensions); nb defaults to ggml's contiguous strides"""
         ne = list(ne) + [1] * (4 - len(ne))
-        return cls(type_, (ctypes.c_int64 * 4)(*ne), int(contiguous))
+        if nb is None:
+            size, blck = GGML_TYPE_BLOCK[type_]
+            nb = [size, size * (ne[0] // blck)]
+            nb += [nb[1] * ne[1], nb[1] * ne[1] * ne[2]]
+        nb = list(nb) + [0] * (4 - len(nb))
+        return cls(type_, (ctypes.c_int64 * 4)(*ne), int(contiguous), (ctypes.c_size_t * 4)(*nb))
+
+    @classmethod
+    def of_tensor(cls, t):
+        """ggml view of a torch tensor of up to four dimensions: ne reversed from
+        its shape, nb from its strides (in bytes), ggml's order"""
+        import torch
+        types = {torch.float32: GGML_F32, torch.float16: GGML_F16, torch.int32: GGML_I32}
+        es = t.element_size()
+        ne = list(reversed(t.shape)) + [1] * (4 - t.dim())
+        nb = [st * es for st in reversed(t.stride())]
+        for d in range(t.dim(), 4):  # missing outer dimensions: ggml's contiguous extension
+            nb.append(nb[-1] * ne[d - 1] if nb else es)
+        return cls(types[t.dtype], (ctypes.c_int64 * 4)(*ne), int(t.is_contiguous()), (ctypes.c_size_t * 4)(*nb))
 
 
 class Exl3Error(RuntimeError):
@@ -116,6 +143,16 @@ def load(path=LIB_PATH):
     ti = ctypes.POINTER(TensorInfo)
     L.exl3_hip_supports_op.restype = i
     L.exl3_hip_supports_op.argtypes = [i, ti, ti, ti]
+    L.exl3_hip_mul_mat_nd.restype = i
+    L.exl3_hip_mul_mat_nd.argtypes = [vp, u, u, sz, sz, vp, ti, vp, ti, vp, sz, st]
+    L.exl3_hip_get_rows_nd.restype = i
+    L.exl3_hip_get_rows_nd.argtypes = [vp, u, u, sz, sz, vp, ti, vp, ti, vp, st]
+    L.exl3_hip_workspace_status.restype = i
+    L.exl3_hip_workspace_status.argtypes = [vp, sz, ctypes.POINTER(i), st]
+    L.exl3_hip_test_exchange_fault.restype = i
+    L.exl3_hip_test_exchange_fault.argtypes = [i, i]
+    L.exl3_hip_mul_mat_group_workspace_bytes.restype = sz
+    L.exl3_hip_mul_mat_group_workspace_bytes.argtypes = [sz, ctypes.POINTER(sz), sz, sz]
     L.exl3_hip_model_embedding_tables.restype = i
     L.exl3_hip_model_embedding_tables.argtypes = [vp, ctypes.POINTER(sz), ctypes.c_char_p, sz]
     L.exl3_hip_model_embedding_table.restype = i
@@ -159,6 +196,20 @@ def new_workspace(k, n, rows, device="cuda"):
     ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
     _check(lib().exl3_hip_workspace_init(_ptr(ws), nbytes, _stream()), "workspace_init")
     return ws
+
+
+def workspace_faulted(workspace=None, stream=None):
+    """exl3_hip_workspace_status: True when a split-K hand-off with this workspace (None:
+    the internal one of this stream) gave up waiting; clear with workspace_init"""
+    f = ctypes.c_int()
+    wb = workspace.numel() if workspace is not None else 0
+    _check(lib().exl3_hip_workspace_status(_ptr(workspace), wb, ctypes.byref(f), _stream(stream)), "workspace_status")
+    return bool(f.value)
+
+
+def workspace_init(workspace=None, stream=None):
+    wb = workspace.numel() if workspace is not None else 0
+    _check(lib().exl3_hip_workspace_init(_ptr(workspace), wb, _stream(stream)), "workspace_init")
 
 
 def mul_mat(records, bits, k, n, x, codebook=CB_MUL1, out_dtype=None, y=None, workspace=None, stream=None,
@@ -272,6 +323,32 @@ def get_rows(records, bits, k, n, ids, codebook=CB_MUL1, out_dtype=None, out=Non
     _check(lib().exl3_hip_get_rows(_ptr(records), bits, codebook, k, n, _ptr(ids), count, _ptr(out), ot,
                                    out.stride(0), _ptr(bad_ids), _stream(stream)), "get_rows")
     return out
+
+
+def mul_mat_nd(records, bits, k, n, x, y, codebook=CB_MUL1, workspace=None, stream=None):
+    """The ggml op on ggml views (exl3_hip_mul_mat_nd): x is a torch tensor of up to four
+    dimensions whose last dimension (ggml's ne[0]) is k and dense, y the same shape with n;
+    both may be permuted or sliced views.  Every row of x is multiplied into the row of y
+    with the same indices, the rows addressed as the reference's row_offset does."""
+    xi, yi = TensorInfo.of_tensor(x), TensorInfo.of_tensor(y)
+    ws_ptr, ws_bytes = (None, 0) if workspace is None else (_ptr(workspace), workspace.numel())
+    _check(lib().exl3_hip_mul_mat_nd(_ptr(records), bits, codebook, k, n, _ptr(x), ctypes.byref(xi), _ptr(y),
+                                     ctypes.byref(yi), ws_ptr, ws_bytes, _stream(stream)), "mul_mat_nd")
+    return y
+
+
+def get_rows_nd(records, bits, k, n, ids, out, codebook=CB_MUL1, bad_ids=None, stream=None):
+    """GET_ROWS on ggml views (exl3_hip_get_rows_nd): ids an int32 tensor of up to three
+    dimensions (any strides), out of shape ids.shape + (k,) (any disjoint row strides)."""
+    ii, oi = TensorInfo.of_tensor(ids), TensorInfo.of_tensor(out)
+    _check(lib().exl3_hip_get_rows_nd(_ptr(records), bits, codebook, k, n, _ptr(ids), ctypes.byref(ii), _ptr(out),
+                                      ctypes.byref(oi), _ptr(bad_ids), _stream(stream)), "get_rows_nd")
+    return out
+
+
+def group_workspace_bytes(k, ns, rows):
+    arr = (ctypes.c_size_t * len(ns))(*ns)
+    return lib().exl3_hip_mul_mat_group_workspace_bytes(k, arr, len(ns), rows)
 
 
 class Model:
