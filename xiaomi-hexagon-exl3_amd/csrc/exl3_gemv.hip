@@ -604,6 +604,11 @@ void set_exchange_fault(int spin_limit, int drop_split) {
     g_fault_spin_limit.store(spin_limit > 0 ? spin_limit : 0, std::memory_order_relaxed);
     g_fault_drop_split.store(drop_split >= 0 ? drop_split : -1, std::memory_order_relaxed);
 }
+int exchange_spin_limit() {
+    const int spin = g_fault_spin_limit.load(std::memory_order_relaxed);
+    return spin > 0 ? spin : kExchangeSpinLimit;
+}
+int exchange_drop_split() { return g_fault_drop_split.load(std::memory_order_relaxed); }
 
 template <int K, int CB>
 static hipError_t launch_gemv_kc(const GemvTargets &tg, const void *x, int x_f16, size_t rows, size_t x_stride,
@@ -615,9 +620,8 @@ static hipError_t launch_gemv_kc(const GemvTargets &tg, const void *x, int x_f16
     const int kq = p.kbs / p.splits, kr = p.kbs % p.splits;
     uint32_t *part = (uint32_t *)(ws + p.partials_off);
     uint32_t *status = (uint32_t *)(ws + kStatusOffset);
-    const int spin = g_fault_spin_limit.load(std::memory_order_relaxed);
-    const int spin_limit = spin > 0 ? spin : kExchangeSpinLimit;
-    const int drop_split = g_fault_drop_split.load(std::memory_order_relaxed);
+    const int spin_limit = exchange_spin_limit();
+    const int drop_split = exchange_drop_split();
     if (rows > 16) {
         uint16_t *xp = (uint16_t *)(ws + p.xpre_off);
         gemv_xprep_kernel<<<dim3((unsigned)((rows + 3) / 4), (unsigned)p.kbs, (unsigned)tg.count), dim3(256), 0,

@@ -47,6 +47,8 @@ constexpr size_t kSharedPrefixBytes = kGemvExchangeBytes + kStatusBytes;
 // polls per wave); drop_split >= 0 makes that split's workgroups skip storing
 // their partial.  set_exchange_fault(0, -1) restores the defaults.
 void set_exchange_fault(int spin_limit, int drop_split);
+int exchange_spin_limit();   // the wait budget of the split-K hand-off (polls per wave)
+int exchange_drop_split();   // -1 unless a test dropped a split
 
 // Up to kGemvMaxTargets matrices that share k, the bit rate, the codebook and x,
 // served by one GEMV launch: column groups [nb_end[i-1], nb_end[i]) belong to
