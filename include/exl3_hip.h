@@ -201,7 +201,10 @@ exl3_status exl3_hip_mul_mat(const void *records, unsigned bits, unsigned codebo
  * enqueued.  Every call on a GPU shares
  * that GPU's array: calls that overlap on one GPU (different streams, or
  * threads without ordering) race and give wrong results; order them on one
- * stream.  Results equal exl3_hip_mul_mat's bit for bit. */
+ * stream.  Results equal exl3_hip_mul_mat's bit for bit.  A split-K wait that
+ * gives up (see exl3_hip_workspace_status) marks the array like any workspace;
+ * the array cannot be zero-filled again from outside, so every later call on
+ * that GPU that sums split partials writes NaN until the process ends. */
 exl3_status exl3_hip_mul_mat_noalloc(const void *records, unsigned bits, unsigned codebook, size_t k, size_t n,
                                      const void *x, exl3_dtype xt, size_t rows, size_t x_row_stride,
                                      void *y, exl3_dtype yt, size_t y_row_stride, hipStream_t stream);
