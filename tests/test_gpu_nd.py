@@ -124,3 +124,42 @@ def test_get_rows_nd_views(amd, oracle, odt):
     else:
         assert np.array_equal(got.view(np.uint16), want.astype(np.float16).view(np.uint16))
     assert torch.all(obase[:, :, :32] == 3.0) and torch.all(obase[:, :, 32 + k:] == 3.0)
+
+
+def test_mul_mat_nd_random_views(amd, oracle):
+    """Seeded random 4-D views: x and y each a permutation of their three row
+    dimensions, sliced from larger buffers (gaps between rows and slices), fp16 or
+    fp32 x; every row checked against the oracle through row_offset, and nothing
+    outside y's view written."""
+    import itertools
+    import torch
+    k, n, bits = 512, 384, 3
+    rec = make_layer(91, k, n, bits)
+    rd = dev(rec)
+    rng = np.random.default_rng(2026)
+    perms = list(itertools.permutations(range(3)))
+    for case in range(12):
+        shape = tuple(int(v) for v in rng.integers(1, 4, size=3))   # row dimensions (outer .. inner)
+        xdt = torch.float16 if case % 2 == 0 else torch.float32
+        npdt = np.float16 if xdt == torch.float16 else np.float32
+        g = torch.Generator().manual_seed(100 + case)
+        px, py = perms[int(rng.integers(len(perms)))], perms[int(rng.integers(len(perms)))]
+        pad_x = tuple(int(v) for v in rng.integers(0, 2, size=3))
+        pad_y = tuple(int(v) for v in rng.integers(0, 2, size=3))
+        # buffers laid out in the permuted order, one spare slice per padded dimension
+        xs = tuple(shape[p] + pad_x[i] for i, p in enumerate(px))
+        ys = tuple(shape[p] + pad_y[i] for i, p in enumerate(py))
+        xbase = torch.randn(*xs, k + 32, generator=g).to(xdt).cuda()
+        ybase = torch.full((*ys, n + 64), 7.0, dtype=torch.float32).cuda()
+        inv_x, inv_y = np.argsort(px), np.argsort(py)
+        xv = xbase[tuple(slice(0, shape[p]) for p in px) + (slice(16, 16 + k),)].permute(*inv_x, 3)
+        yv = ybase[tuple(slice(0, shape[p]) for p in py) + (slice(0, n),)].permute(*inv_y, 3)
+        assert tuple(xv.shape) == shape + (k,) and tuple(yv.shape) == shape + (n,)
+        print(f"  random view {case}: rows {shape} x perm {px} y perm {py} x={xdt}", flush=True)
+        amd.mul_mat_nd(rd, bits, k, n, xv, yv)
+        torch.cuda.synchronize()
+        want = oracle.mul_mat(rec, bits, 2, k, n, gather_rows(xbase, xv, k, npdt).astype(np.float32))
+        assert_layer_close(gather_rows(ybase, yv, n, np.float32), want, what=f"random view {case}")
+        mask = torch.ones_like(ybase, dtype=torch.bool)
+        mask[tuple(slice(0, shape[p]) for p in py) + (slice(0, n),)] = False
+        assert torch.all(ybase[mask] == 7.0), f"random view {case}: bytes outside the view written"
