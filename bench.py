@@ -53,6 +53,8 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="skip the C1/C2/C4/GET_ROWS lines")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only time a plain device copy of COPY_BYTES (scales the HBM byte counters)")
+    ap.add_argument("--dense-gemm", action="store_true",
+                    help="only time the library's dense fp16 GEMM of the M=512 shape (for profiling)")
     return ap.parse_args()
 
 
@@ -82,6 +84,34 @@ def calib_copy(args):
                       "gbps_read_plus_write": round(2 * COPY_BYTES / (us * 1e-6) / 1e9, 1)}), flush=True)
 
 
+DENSE_COPIES = 5   # dense fp16 copies of the 4096 x 14336 weight, 117 MB each: 587 MB rotated
+
+
+def dense_gemm(torch, stream, steps):
+    """The M=512 product on dense fp16 weights through torch.matmul (hipBLASLt on
+    ROCm): x[512, k] @ W[n, k]^T, rotating through DENSE_COPIES weight copies as
+    the EXL3 calls rotate through theirs, so that each call reads its weights
+    from HBM.  Not the EXL3 layer (no decode, no rotations, 4x the weight bytes):
+    the rate the vendor's tuned library reaches on an fp16 GEMM of this shape on
+    the same GPU, beside the EXL3 GEMM's."""
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    x = torch.randn(512, K_IN, generator=gen, dtype=torch.float16, device="cuda")
+    w = [torch.randn(N_OUT, K_IN, generator=gen, dtype=torch.float16, device="cuda") for _ in range(DENSE_COPIES)]
+    y = torch.empty(512, N_OUT, dtype=torch.float16, device="cuda")
+    turn = [0]
+
+    def fn():
+        torch.matmul(x, w[turn[0] % DENSE_COPIES].t(), out=y)
+        turn[0] += 1
+    for _ in range(2 * DENSE_COPIES):
+        fn()
+    per_graph = max(DENSE_COPIES * 4, steps // DENSE_COPIES * DENSE_COPIES)
+    ms = graph_time(torch, stream, fn, per_graph)
+    del w
+    return {"call_us": round(ms * 1e3, 1), "tflops": round(2.0 * 512 * K_IN * N_OUT / (ms * 1e-3) / 1e12, 1),
+            "weight_copies": DENSE_COPIES}
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -105,6 +135,9 @@ def main():
     stream = torch.cuda.current_stream()
     if args.only_c1:
         print(json.dumps(extra_configs(amd, torch, np, synth, stream, args, only_c1=True)), flush=True)
+        return
+    if args.dense_gemm:
+        print(json.dumps({"dense_fp16_gemm_m512": dense_gemm(torch, stream, args.steps)}), flush=True)
         return
 
     # ---- synthetic layer, 18 resident copies
@@ -231,7 +264,8 @@ def main():
         flops = 2.0 * 512 * K_IN * N_OUT
         tflops = flops / (msg * 1e-3) / 1e12
         extra["gemm_m512"] = {"tflops": round(tflops, 1), "call_us": round(msg * 1e3, 1),
-                              "frac_mfma": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+                              "frac_mfma": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                              "dense_fp16_library": dense_gemm(torch, stream, gsteps)}
 
     if not args.only_gemv and not args.no_extra:
         extra.update(extra_configs(amd, torch, np, synth, stream, args))
