@@ -499,7 +499,8 @@ __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu
         // a partial may still arrive, so the status word marks the workspace
         __syncthreads();
         if (tid == 0 && *gave_up && !poisoned) __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        for (int t = tid; t < nsp * nval; t += NT) clear_exchange(all + t);
+        // nval is a multiple of 128 words and `all` 512-byte aligned: whole 16-byte units
+        for (int t = 4 * tid; t < nsp * nval; t += 4 * NT) clear_exchange4(all + t);
         return;
     }
     // 6. (one workgroup per column group) output H128 per row from the LDS sums
