@@ -55,6 +55,9 @@ def parse():
                     help="only time a plain device copy of COPY_BYTES (scales the HBM byte counters)")
     ap.add_argument("--dense-gemm", action="store_true",
                     help="only time the library's dense fp16 GEMM of the M=512 shape (for profiling)")
+    ap.add_argument("--stamps", action="store_true",
+                    help="GEMV phase stamps from libexl3_hip_stamps.so: the C3 layer at --only-rows rows "
+                         "(default 1), or the k=2048 x n=6144 layer with --only-c1")
     return ap.parse_args()
 
 
@@ -82,6 +85,76 @@ def calib_copy(args):
     us = a.elapsed_time(b) * 1e3 / args.steps
     print(json.dumps({"calib_copy_bytes": COPY_BYTES, "us_per_copy": round(us, 2),
                       "gbps_read_plus_write": round(2 * COPY_BYTES / (us * 1e-6) / 1e9, 1)}), flush=True)
+
+
+STAMP_PHASES = ["start", "prep barrier passed", "main loops done (all waves)", "partial ready",
+                "summing: other splits' words read", "summing: y issued", "summing: exchange cleared"]
+
+
+def phase_stamps(args):
+    """Where one GEMV call's time goes, from the diagnostic twin of the library
+    (libexl3_hip_stamps.so: the same kernels plus one 64-bit store of the
+    100 MHz s_memrealtime counter by thread 0 of every workgroup at each phase).
+    A graph of back-to-back calls over rotated weight copies runs as in the
+    timed bench; the stamps of its last call are read back and reported in us
+    from the first workgroup's start, p50 / p90 / max over the workgroups of
+    each kind: all, a CU's first and second workgroup (blocks below and above
+    half the grid when the grid is two per CU), the summing workgroups."""
+    import ctypes
+    import importlib.util
+
+    import numpy as np
+    import torch
+
+    import synth
+    spec = importlib.util.spec_from_file_location("exl3_amd_stamps", ROOT / "xiaomi-hexagon-exl3_amd" / "exl3_amd.py")
+    amd = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(amd)
+    amd._LIB = amd.load(ROOT / "xiaomi-hexagon-exl3_amd" / "libexl3_hip_stamps.so")
+    read = amd._LIB.exl3_hip_debug_gemv_stamps
+    read.restype, read.argtypes = ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t]
+    k, n, copies = (2048, 6144, 48) if args.only_c1 else (K_IN, N_OUT, COPIES)
+    rows = args.only_rows or 1
+    dev = torch.device("cuda", 0)
+    p = synth.packed_tiles(77, k, n, BITS)
+    su, sv = synth.layer_scales(77, k, n)
+    rec = torch.from_numpy(synth.pack_records(p, su, sv, BITS).view(np.uint8).copy()).to(dev)
+    recs = [rec] + [rec.clone() for _ in range(copies - 1)]
+    x = torch.from_numpy(synth.activations(1000 + rows, rows, k)).to(dev)
+    y = torch.empty((rows, n), dtype=torch.float16, device=dev)
+    ws = amd.new_workspace(k, n, rows)
+    turn = [0]
+
+    def fn():
+        amd.mul_mat(recs[turn[0] % copies], BITS, k, n, x, codebook=CB, y=y, workspace=ws)
+        turn[0] += 1
+    ms = graph_time(torch, torch.cuda.current_stream(), fn, 2 * copies)
+    torch.cuda.synchronize()
+    st = np.zeros((8192, 8), dtype=np.uint64)
+    if read(st.ctypes.data, st.size) != 0:
+        raise RuntimeError("reading the phase stamps failed")
+    used = np.nonzero(st[:, 0])[0]
+    if used.size == 0:
+        raise RuntimeError(f"rows {rows}: the call ran no GEMV workgroup (above the GEMV's row range?)")
+    G, nbs = int(used.max()) + 1, n // 128
+    splits = G // nbs
+    t0 = int(st[:G, 0].min())
+    us = (st[:G].astype(np.int64) - t0) / 100.0   # 100 MHz ticks -> us
+
+    def q(v):
+        return [round(float(np.percentile(v, 50)), 2), round(float(np.percentile(v, 90)), 2), round(float(v.max()), 2)]
+    summing = np.arange(G) >= (splits - 1) * nbs
+    first = np.arange(G) < G // 2
+    out = {"workload": f"EXL3 GEMV k={k} x n={n}, 4 bpw, rows {rows}", "workgroups": G, "splits": splits,
+           "call_us_stamps_build": round(ms * 1e3, 2), "unit": "us from the first workgroup's start, p50/p90/max",
+           "phases": {}}
+    for ph, name in enumerate(STAMP_PHASES):
+        if ph < 4:
+            out["phases"][name] = {"all": q(us[:, ph]), "first_on_cu": q(us[first, ph]),
+                                   "second_on_cu": q(us[~first, ph]), "summing": q(us[summing, ph])}
+        else:
+            out["phases"][name] = {"summing": q(us[summing, ph])}
+    print(json.dumps({"gemv_phase_stamps": out}), flush=True)
 
 
 DENSE_COPIES = 5   # dense fp16 copies of the 4096 x 14336 weight, 117 MB each: 587 MB rotated
@@ -121,6 +194,9 @@ def main():
         sys.exit(2)
     if args.calib_copy:
         calib_copy(args)
+        return
+    if args.stamps:
+        phase_stamps(args)
         return
 
     import numpy as np

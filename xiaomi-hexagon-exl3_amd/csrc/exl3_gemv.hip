@@ -47,6 +47,44 @@ template <int K>
 struct GemvStream {
     static constexpr int DEPTH = K <= 2 ? 12 : (K <= 4 ? 8 : 4);  // groups in flight per wave
 };
+// Phase stamps, in the diagnostic library only (libexl3_hip_stamps.so, built with
+// EXL3_PHASE_STAMPS): at each phase of the call thread 0 of the workgroup puts
+// the 100 MHz s_memrealtime counter into a 64-byte LDS slot, and at its end
+// copies the slot to g_exl3_gemv_stamps[workgroup][phase] (workgroup = x + nbs
+// y in dispatch order) with ordinary vector stores: no global store sits
+// between the phases for a later wait on memory to include, and no register
+// stays live across the kernel for the stamps.  Every call overwrites what its
+// workgroups reach; after a stream of equal calls the array holds the last
+// one.  Phases: 0 start, 1 prep barrier passed, 2 every wave's main loop done,
+// 3 partial ready (a writer: its words issued; the summing workgroup: its own
+// partial in LDS), 4 the other splits' words of row 0 read, 5 row 0's output
+// issued, 6 the exchange cleared (4..6: summing workgroups only).
+#ifdef EXL3_PHASE_STAMPS
+constexpr int kStampPhases = 8;
+constexpr unsigned kStampWorkgroups = 8192;
+__device__ uint64_t g_exl3_gemv_stamps[kStampWorkgroups * kStampPhases];
+struct PhaseStamps {
+    uint64_t *slot;
+    __device__ __forceinline__ void mark(int phase) {
+        if (threadIdx.x == 0) slot[phase] = __builtin_amdgcn_s_memrealtime();
+    }
+    __device__ __forceinline__ void flush(int phases) {
+        const unsigned w = blockIdx.x + gridDim.x * blockIdx.y;
+        if (threadIdx.x == 0 && w < kStampWorkgroups)
+            for (int p = 0; p < phases; ++p) g_exl3_gemv_stamps[w * kStampPhases + p] = slot[p];
+    }
+};
+#define EXL3_STAMPS_DECLARE                                    \
+    __shared__ uint64_t stamp_slot[kStampPhases];              \
+    PhaseStamps stamps{stamp_slot};
+#else
+struct PhaseStamps {
+    __device__ __forceinline__ void mark(int) {}
+    __device__ __forceinline__ void flush(int) {}
+};
+#define EXL3_STAMPS_DECLARE PhaseStamps stamps;
+#endif
+
 constexpr int kGemvPrepMax = 16;          // a workgroup preps at most kGemvPrepMax x waves (kb, row) blocks
 constexpr size_t kGemvDummyBytes = 8192;  // >= largest lane offset of a group + its K words (1024 K)
 constexpr size_t kGemvFragLds = 49152;    // LDS budget of the B fragments of a workgroup (rows <= 8)
@@ -86,6 +124,8 @@ __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu
     // grid (column group, split): no division on the way to the first loads.
     // Split s owns kq + (s < kr) records from kb0 (kq = kbs / splits, kr = kbs % splits)
     const int nb = blockIdx.x, s = blockIdx.y;
+    EXL3_STAMPS_DECLARE
+    stamps.mark(0);
     // The 9..16-row prep (hi and lo fragments of up to 16 rows) is long enough
     // that, at equal priority, a CU's second workgroup runs it mostly in the
     // issue gaps of the first one's decode (the older waves issue first): raised
@@ -290,6 +330,7 @@ __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu
     }
     const float sv0 = half_bits_to_float(svp[lane]), sv1 = half_bits_to_float(svp[lane + 64]);
     __syncthreads();
+    stamps.mark(1);
     if constexpr (MODE == 1) __builtin_amdgcn_s_setprio(0);
     if (MODE == 2 || nblk <= W) load_chunk<K>(group_src(0), buf[0]);  // not issued by the prep
 #pragma unroll
@@ -345,6 +386,7 @@ __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu
     // 5. epilogue: hi + lo (MFMA column m < 8 gets column m + 8) into this wave's
     // 32 columns of its share of the workgroup partial (MODE 2: column m is row m)
     __syncthreads();  // every wave is done with the fragments; LDS now holds the partials
+    stamps.mark(2);
     float *red = (float *)smem;  // [P][rows][128]
     const int nval = rows * 128;
 #pragma unroll
@@ -431,6 +473,8 @@ __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu
                 const int t = tid + i * NT;
                 if (t < nval) store_exchange(mine + t, psum[i]);
             }
+            stamps.mark(3);
+            stamps.flush(4);
             return;
         }
         // the last split: wave r sums row r's elements lane and lane + 64 over
@@ -449,6 +493,7 @@ __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu
         }
         if (tid == 0) *gave_up = poisoned != 0u;
         __syncthreads();
+        stamps.mark(3);
         const int nsp = splits - 1;  // splits in the exchange
         int budget = spin_limit;
         for (int rr = wave; rr < rows; rr += W) {
@@ -493,7 +538,9 @@ __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu
                         a1 += v1[jb] && !poisoned ? exchange_value(v1[jb]) : __builtin_nanf("");
                     }
             }
+            if (rr == 0) stamps.mark(4);
             finish_row(rr, a0 + own[rr * 128 + lane], a1 + own[rr * 128 + lane + 64]);
+            if (rr == 0) stamps.mark(5);
         }
         // every word has been read: empty them for the next call; after a give-up
         // a partial may still arrive, so the status word marks the workspace
@@ -501,6 +548,8 @@ __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu
         if (tid == 0 && *gave_up && !poisoned) __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         // nval is a multiple of 128 words and `all` 512-byte aligned: whole 16-byte units
         for (int t = 4 * tid; t < nsp * nval; t += 4 * NT) clear_exchange4(all + t);
+        stamps.mark(6);
+        stamps.flush(7);
         return;
     }
     // 6. (one workgroup per column group) output H128 per row from the LDS sums
@@ -510,7 +559,9 @@ __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu
         if (t < nval) own[t] = psum[i];
     }
     __syncthreads();
+    stamps.mark(3);
     for (int rr = wave; rr < rows; rr += W) finish_row(rr, own[rr * 128 + lane], own[rr * 128 + lane + 64]);
+    stamps.flush(4);
 }
 
 // Activations of the 17..32-row GEMV (MODE 2): fp16(H128(x[r] su)), su from record
@@ -683,3 +734,15 @@ hipError_t launch_gemv(const void *records, int bits, int cb, size_t k, size_t n
 }
 
 }  // namespace exl3k
+
+#ifdef EXL3_PHASE_STAMPS
+// The diagnostic library's one extra export: copies up to `count` stamps
+// ([workgroup][8 phases], 100 MHz ticks) of the current device into `out`.
+extern "C" __attribute__((visibility("default"))) int exl3_hip_debug_gemv_stamps(uint64_t *out, size_t count) {
+    const size_t all = (size_t)exl3k::kStampWorkgroups * exl3k::kStampPhases;
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(exl3k::g_exl3_gemv_stamps), (count < all ? count : all) * 8) ==
+                   hipSuccess
+               ? 0
+               : -1;
+}
+#endif
