@@ -71,8 +71,9 @@ const char *exl3_hip_status_string(exl3_status status);
 
 /* Largest row count served by the register-decode GEMV kernel (32): a grouped
  * call (exl3_hip_mul_mat_group) of at most this many rows is one GEMV launch.
- * exl3_hip_mul_mat runs the GEMV up to 14 rows and the LDS-decode MFMA GEMM
- * kernel above, where the GEMM is the faster of the two. */
+ * exl3_hip_mul_mat runs the GEMV up to 14 rows (16 when a GEMV workgroup's
+ * share of k is short: at most 64 (record, row) blocks to prepare) and the
+ * LDS-decode MFMA GEMM kernel above, where the GEMM is the faster of the two. */
 size_t exl3_hip_gemv_max_rows(void);
 
 /* 1 when exl3_hip_mul_mat accepts this problem: bits 1..8, codebook 0..2,

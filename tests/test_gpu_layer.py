@@ -77,6 +77,24 @@ def test_c3_full_size_gemv(amd, oracle, rows):
         assert rl < 1e-5  # hi/lo activation split keeps the GEMV at fp32-level accuracy
 
 
+@pytest.mark.parametrize("k,n,bits", [(2048, 2048, 6), (2048, 512, 6), (6144, 2048, 3), (14336, 4096, 4)])
+@pytest.mark.parametrize("rows", [15, 16])
+def test_rows_15_16_short_k_on_gemv(amd, oracle, k, n, bits, rows):
+    """One matrix at 15..16 rows runs the two-block hi/lo GEMV when a GEMV
+    workgroup prepares at most 64 (record, row) blocks (short k: the q/k/v/o,
+    gate/up and down projections of the 2B model), the GEMM's 32-row tiles
+    otherwise (k = 14336).  The hi/lo split shows in the accuracy: rel-L2 < 1e-5
+    on the GEMV against ~3e-4 with the GEMM's fp16 activations."""
+    rec = make_layer(420 + k // 128 + rows, k, n, bits)
+    x = synth.activations(421 + rows, rows, k)
+    ref = oracle.mul_mat(rec, bits, 2, k, n, x, threads=THREADS)
+    ma, rl = assert_layer_close(run(amd, dev(rec), bits, k, n, x), ref, what=f"k={k} n={n} rows={rows}")
+    if k <= 8192:
+        assert rl < 1e-5
+    else:
+        assert rl > 1e-5  # the GEMM: fp16 activations
+
+
 @pytest.mark.parametrize("rows", [33, 37, 128, 300])
 def test_gemm_rows(amd, oracle, rows):
     k, n, bits = 1024, 384, 4

@@ -255,7 +255,7 @@ static exl3_status mul_mat_impl(const void *records, unsigned bits, unsigned cod
     if (!records || !x || !y || !aligned(records, 16)) return EXL3_INVAL_PARAMS;
     if (!aligned(x, dtype_size(xt)) || !aligned(y, dtype_size(yt))) return EXL3_INVAL_PARAMS;
     if (x_row_stride < k || y_row_stride < n) return EXL3_INVAL_PARAMS;
-    const bool gemv = rows <= (size_t)exl3k::kGemvSingleMaxRows && exl3k::gemv_serves(k, n, rows);
+    const bool gemv = exl3k::gemv_serves_single(k, n, rows);
     const size_t need = exl3_hip_mul_mat_workspace_bytes(k, n, rows);
     if (workspace) {
         if (!aligned(workspace, 256)) return EXL3_INVAL_PARAMS;
@@ -327,7 +327,7 @@ exl3_status exl3_hip_mul_mat_group(const exl3_matrix_desc *mats, size_t count, u
     }
     // GEMM (or, for one matrix above the single-matrix GEMV rows, whichever
     // exl3_hip_mul_mat picks): one call per matrix, each a full-size launch
-    if (!exl3k::gemv_serves(k, n_total, rows) || (count == 1 && rows > (size_t)exl3k::kGemvSingleMaxRows)) {
+    if (!exl3k::gemv_serves(k, n_total, rows) || (count == 1 && !exl3k::gemv_serves_single(k, n_total, rows))) {
         for (size_t i = 0; i < count; ++i) {
             const exl3_status st = exl3_hip_mul_mat(mats[i].records, bits, codebook, k, mats[i].n, x, xt, rows,
                                                     x_row_stride, mats[i].y, yt, mats[i].y_row_stride, workspace,

@@ -650,6 +650,13 @@ bool gemv_serves(size_t k, size_t n, size_t rows) {
     return rows >= 1 && rows <= (size_t)kGemvMaxRows && gemv_plan(k, n, rows).fits;
 }
 
+bool gemv_serves_single(size_t k, size_t n, size_t rows) {
+    if (!gemv_serves(k, n, rows)) return false;
+    if (rows <= (size_t)kGemvSingleMaxRows) return true;
+    // rows 15..16 (the two-block hi/lo GEMV) when a workgroup's prep is short
+    return rows <= 16 && (size_t)gemv_plan(k, n, rows).nkw * rows <= (size_t)kGemvSinglePrepBlocks;
+}
+
 static std::atomic<int> g_fault_spin_limit{0}, g_fault_drop_split{-1};
 
 void set_exchange_fault(int spin_limit, int drop_split) {

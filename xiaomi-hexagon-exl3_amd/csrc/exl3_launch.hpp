@@ -14,10 +14,16 @@ namespace exl3k {
 // A single matrix above kGemvSingleMaxRows rows runs the GEMM (32-row tiles up to
 // 32 rows), which is flat in the row count from there (k = 14336, n = 4096:
 // 21.2-21.5 us for rows 14..32, against the GEMV's 21.4 at 14 rows, 22.4 at 16,
-// 24.5 at 20); a grouped call keeps its one GEMV launch up to kGemvMaxRows rows
-// (q/k/v at 32 rows: 18 us against 41 us for three GEMM calls).
+// 24.5 at 20), except at 15..16 rows when a GEMV workgroup's prep is at most
+// kGemvSinglePrepBlocks (record, row) blocks: there the hi/lo GEMV is faster
+// (rows 16: k = 2048, n = 2048, 6 bits 10.4 against 13.6 us; k = 2048, n = 6144
+// 12.0 against 13.8; k = 6144, n = 2048, 3 bits 12.4 against 14.5), at k = 14336
+// it is not (22.3 against 21.5-21.8 us, 112 blocks).  A grouped call keeps its
+// one GEMV launch up to kGemvMaxRows rows (q/k/v at 32 rows: 18 us against 41 us
+// for three GEMM calls).
 constexpr int kGemvMaxRows = 32;
 constexpr int kGemvSingleMaxRows = 14;
+constexpr int kGemvSinglePrepBlocks = 64;
 constexpr int kGemvWaves = 8;     // waves per GEMV workgroup (a multiple of 4)
 
 // Every plan starts with the same region, which only the GEMV's split-K hand-off
@@ -87,6 +93,9 @@ struct GemmPlan {
 GemvPlan gemv_plan(size_t k, size_t n, size_t rows);
 // rows <= kGemvMaxRows and the GEMV's split partials fit the exchange
 bool gemv_serves(size_t k, size_t n, size_t rows);
+// the GEMV for one matrix: up to kGemvSingleMaxRows rows, and at 15..16 rows where
+// a workgroup preps at most kGemvSinglePrepBlocks (record, row) blocks
+bool gemv_serves_single(size_t k, size_t n, size_t rows);
 GemmPlan gemm_plan(size_t k, size_t n, size_t rows);
 int gemm_tile_rows(size_t rows);
 
