@@ -11,7 +11,8 @@ matrices of the reference fixture geometry (tests/generate_cuda_fixtures.py:
 original-basis weights come from this library's reconstruct and must match the
 reference's reconstruct digest bit for bit before they serve as the float64
 expectation.  The batches reach every launch path at k = 256: the GEMV (1, 4,
-8) and the GEMM's 128- and 512-row tiles without a k split (32, 37, 128, 512).
+8) and the GEMM's 32-, 64-, 128- and 512-row tiles with k split in two records
+(32, 37, 128, 512).
 """
 import hashlib
 import json

@@ -105,15 +105,28 @@ def test_gemm_rows(amd, oracle, rows):
 
 
 @pytest.mark.parametrize("k,n,rows", [(1024, 384, 64), (2048, 640, 48), (512, 384, 40), (1024, 384, 17),
-                                      (2048, 640, 32), (512, 384, 24)])
+                                      (2048, 640, 32), (512, 384, 24), (128, 384, 40), (128, 384, 24)])
 def test_gemm_short_row_tiles(amd, oracle, k, n, rows):
     """Rows 17..32 run 32-row tiles (4 column quarters), rows 33..64 64-row tiles
-    (2 row waves x 4 column quarters); both always split k, and at k = 512 no
-    split is possible (four records per split at least), so the call runs the
-    128-row tile without one."""
+    (2 row waves x 4 column quarters); both always split k (at k = 512 into four
+    splits of one record each), and at k = 128 (one record) no split is
+    possible, so the call runs the 128-row tile without one."""
     bits = 3
     rec = make_layer(410 + rows, k, n, bits)
     x = synth.activations(411 + rows, rows, k)
+    ref = oracle.mul_mat(rec, bits, 2, k, n, x, threads=THREADS)
+    assert_layer_close(run(amd, dev(rec), bits, k, n, x), ref, what=f"GEMM k={k} n={n} rows={rows}")
+
+
+@pytest.mark.parametrize("rows", [100, 200, 300])
+def test_gemm_unsplit_tiles(amd, oracle, rows):
+    """At k = 256, n = 4096 the 128-, 256- and 512-row tiles run without a k split
+    (32 column groups: the split partials would cost more than the second
+    record's decode saves), so each workgroup sums both records and applies H128
+    and sv itself."""
+    k, n, bits = 256, 4096, 4
+    rec = make_layer(420 + rows, k, n, bits)
+    x = synth.activations(421 + rows, rows, k)
     ref = oracle.mul_mat(rec, bits, 2, k, n, x, threads=THREADS)
     assert_layer_close(run(amd, dev(rec), bits, k, n, x), ref, what=f"GEMM k={k} n={n} rows={rows}")
 

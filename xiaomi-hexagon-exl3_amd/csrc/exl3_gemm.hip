@@ -565,6 +565,44 @@ int gemm_tile_rows(size_t rows) {
     return rows <= 32 ? 32 : rows <= 64 ? 64 : rows <= 128 ? 128 : rows <= 256 ? 256 : 512;
 }
 
+// k splits of a tile class: split k only below kGemmSplitTiles tiles (the split
+// partials are summed by gemm_reduce_kernel), at most one split per record.
+// 32- and 64-row tiles fill the CUs once (one workgroup each); 32-row tiles (4
+// waves, 64 KB of LDS) run two per CU when each split keeps >= 4 records (rows
+// 17..32 at k = 14336, n = 4096: 22.7 -> 21.2 us; at k <= 6144 two per CU with
+// 1..2 records each were 1.5-3 us slower than one).  For 128..512-row tiles
+// the count minimises records per split x the tile's measured time per record
+// (1.15 / 1.73 / 2.83 us) + split-partial bytes at 0.6 us per MB (written by
+// the GEMM, read by the reduction), within one workgroup per CU.  Measured
+// sweeps over splits 1..32 (k = 2048 / 6144 / 14336, n = 512..6144, rows
+// 24..512) put this rule within 1 us of each shape's best count; against at
+// least 4 records per split it takes k = 2048, n = 512 at rows 300 from 23.4
+// to 18.8 us and k = 2048, n = 2048 at rows 24 from 13.7 to 11.6 us.
+static int gemm_splits(int kbs, int tiles, int bm) {
+    if (tiles >= (int)kGemmSplitTiles) return 1;
+    int s;
+    if (bm <= 64) {
+        int wgs = kGemmTargetWgs;
+        if (bm == 32 && kbs / ((2 * kGemmTargetWgs + tiles - 1) / tiles) >= 4) wgs = 2 * kGemmTargetWgs;
+        s = 2 * tiles > wgs ? (wgs + tiles - 1) / tiles : wgs / tiles;
+        if (s < kbs) {  // the fewest splits with the same records per split
+            const int per = (kbs + s - 1) / s;
+            s = (kbs + per - 1) / per;
+        }
+    } else {
+        const double per_record_us = bm == 128 ? 1.15 : bm == 256 ? 1.73 : 2.83;
+        const int smax = kGemmTargetWgs / tiles > 1 ? kGemmTargetWgs / tiles : 1;
+        double best = 0.0;
+        s = 1;
+        for (int c = 1; c <= smax && c <= kbs; ++c) {
+            const double partial_mb = c > 1 ? (double)tiles * c * bm * 256 * 1e-6 : 0.0;
+            const double t = per_record_us * ((kbs + c - 1) / c) + 0.6 * partial_mb;
+            if (c == 1 || t < best) best = t, s = c;
+        }
+    }
+    return s < 1 ? 1 : (s > kbs ? kbs : s);
+}
+
 static GemmPlan gemm_plan_bm(size_t k, size_t n, size_t rows, int bm) {
     GemmPlan p{};
     p.nbs = (int)(n / 128);
@@ -572,15 +610,7 @@ static GemmPlan gemm_plan_bm(size_t k, size_t n, size_t rows, int bm) {
     p.bm = bm;
     p.mtiles = (int)((rows + p.bm - 1) / p.bm);
     const int tiles = p.nbs * p.mtiles;
-    // split k only below kGemmSplitTiles tiles; the split partials are summed by
-    // gemm_reduce_kernel
-    // 32-row tiles (4 waves, 64 KB of LDS) run two workgroups per CU: twice the
-    // target there (rows 17..32 at k = 14336, n = 4096: 22.7 -> 21.2 us; four
-    // per CU do not fit and were 28.4 us)
-    const int target = p.bm == 32 ? 2 * kGemmTargetWgs : kGemmTargetWgs;
-    int s = tiles >= (int)kGemmSplitTiles ? 1 : (target + tiles - 1) / tiles;
-    const int smax = p.kbs / 4 > 0 ? p.kbs / 4 : 1;
-    s = s < 1 ? 1 : (s > smax ? smax : s);
+    const int s = gemm_splits(p.kbs, tiles, p.bm);
     if (p.bm < 128 && s == 1) return gemm_plan_bm(k, n, rows, 128);  // the 32/64-row tiles need a split
     p.splits = s;
     size_t off = kSharedPrefixBytes;  // the GEMM leaves the GEMV exchange alone
