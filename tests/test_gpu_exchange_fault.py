@@ -39,7 +39,7 @@ def injected(amd, fn):
 @pytest.mark.parametrize("rows,internal", [(1, False), (12, False), (20, False), (1, True)])
 def test_give_up_is_loud_sticky_and_recoverable(amd, rows, internal):
     import torch
-    k, n, bits = 2048, 1024, 4   # 8 column groups x 16 (8 for the grouped call) k splits
+    k, n, bits = 2048, 1024, 4   # 8 column groups (16 for the grouped call) x 16 k splits
     print(f"  exchange fault rows={rows} internal={internal}", flush=True)
     rec = make_layer(41, k, n, bits)
     x = torch.from_numpy(synth.activations(42 + rows, rows, k)).cuda()

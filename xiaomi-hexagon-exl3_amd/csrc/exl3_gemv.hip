@@ -616,12 +616,17 @@ GemvPlan gemv_plan(size_t k, size_t n, size_t rows) {
     p.nbs = (int)(n / 128);
     p.kbs = (int)(k / 128);
     // about four records per workgroup (a workgroup's fixed latency chain then
-    // stays small against its stream), between 128 and 512 workgroups (one to two
-    // per CU); measured best or within 10 % of best for k = 2048..14336
+    // stays small against its stream), between 256 and 512 workgroups (one to two
+    // per CU), and the fewest splits with the same records per split.  Measured
+    // best or within 0.1 us of the best split count at rows 1 and 8 for k = 2048
+    // (n = 512, 2048, 6144; q/k/v 2048 + 512 + 512 and gate/up 2 x 6144 grouped),
+    // 6144 x 2048, 4096 x 14336 and 14336 x 4096; against a floor of 128
+    // workgroups, k = 6144, n = 2048 -0.3 us and the q/k/v group at rows 8 -0.7 us
     int s = (p.kbs + 3) / 4;
     if (p.nbs * s > 512) s = 512 / p.nbs;
-    if (p.nbs * s < 128) s = (128 + p.nbs - 1) / p.nbs;
+    if (p.nbs * s < 256) s = 256 / p.nbs;
     s = s < 1 ? 1 : (s > p.kbs ? p.kbs : s);
+    s = (p.kbs + (p.kbs + s - 1) / s - 1) / ((p.kbs + s - 1) / s);
     // a workgroup's B fragments must fit its LDS budget and a wave prepares at
     // most kGemvPrepMax (kb, row) blocks; one kb per workgroup always fits
     for (;;) {
