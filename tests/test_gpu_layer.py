@@ -77,6 +77,25 @@ def test_c3_full_size_gemv(amd, oracle, rows):
         assert rl < 1e-5  # hi/lo activation split keeps the GEMV at fp32-level accuracy
 
 
+@pytest.mark.parametrize("k,n,bits", [(14336, 4096, 4), (6144, 2048, 3), (2048, 6144, 4)])
+def test_gemv_rows_match_one_row_bitwise(amd, k, n, bits):
+    """Every row of a 2..14-row GEMV call equals the one-row call of that row bit
+    for bit (fp32 output): each row count prepares H128(x su) with the same
+    roundings and the same fp16 hi/lo split, and each output column sums the same
+    products in the same order.  A prep whose hi and lo came from two different
+    roundings of one value (an fp16 conversion fused with the product for one use
+    and not the other) shows here as single rows that differ."""
+    rec = make_layer(430, k, n, bits)
+    rd = dev(rec)
+    x = synth.activations(431, 14, k)
+    ones = np.concatenate([run(amd, rd, bits, k, n, x[r:r + 1]) for r in range(14)])
+    for rows in (2, 4, 8, 9, 12, 14):
+        y = run(amd, rd, bits, k, n, x[:rows])
+        bad = [r for r in range(rows) if not np.array_equal(y[r], ones[r])]
+        print(f"  k={k} n={n} rows={rows}: rows differing from one-row calls {bad}", flush=True)
+        assert not bad
+
+
 @pytest.mark.parametrize("k,n,bits", [(2048, 2048, 6), (2048, 512, 6), (6144, 2048, 3), (14336, 4096, 4)])
 @pytest.mark.parametrize("rows", [15, 16])
 def test_rows_15_16_short_k_on_gemv(amd, oracle, k, n, bits, rows):

@@ -225,6 +225,40 @@ __device__ __forceinline__ float dpp_block_xor(float v) {
     }
 }
 
+// One cross-lane stage S of the block layout above on eight values per lane, in
+// signed form: the butterfly sgn v + v' (sgn = -1 on the lane holding the upper
+// block) equals sgn (v + sgn v'), so the stage keeps m = m + sgn dpp(m) and the
+// caller multiplies the stage signs into one lane sign at the end.  Each value
+// is one v_fmac_f32 whose first operand is the partner lane's register (DPP),
+// where a separate DPP move and fma take two; the compiler does not fuse them.
+// Every sum is rounded as in the unsigned form (round-to-nearest is
+// sign-symmetric).  The s_nop gives the two wait states a DPP read needs after
+// a VALU write of its register; inside the block each value's register was
+// written eight instructions earlier.
+template <int S>
+__device__ __forceinline__ void dpp_block_stage8(float (&m)[8], float sgn) {
+#define EXL3_FMAC8(CTL)                                                                                          \
+    asm volatile("s_nop 1\n"                                                                                     \
+                 "v_fmac_f32_dpp %0, %0, %8 " CTL " row_mask:0xf bank_mask:0xf\n"                                 \
+                 "v_fmac_f32_dpp %1, %1, %8 " CTL " row_mask:0xf bank_mask:0xf\n"                                 \
+                 "v_fmac_f32_dpp %2, %2, %8 " CTL " row_mask:0xf bank_mask:0xf\n"                                 \
+                 "v_fmac_f32_dpp %3, %3, %8 " CTL " row_mask:0xf bank_mask:0xf\n"                                 \
+                 "v_fmac_f32_dpp %4, %4, %8 " CTL " row_mask:0xf bank_mask:0xf\n"                                 \
+                 "v_fmac_f32_dpp %5, %5, %8 " CTL " row_mask:0xf bank_mask:0xf\n"                                 \
+                 "v_fmac_f32_dpp %6, %6, %8 " CTL " row_mask:0xf bank_mask:0xf\n"                                 \
+                 "v_fmac_f32_dpp %7, %7, %8 " CTL " row_mask:0xf bank_mask:0xf"                                   \
+                 : "+v"(m[0]), "+v"(m[1]), "+v"(m[2]), "+v"(m[3]), "+v"(m[4]), "+v"(m[5]), "+v"(m[6]), "+v"(m[7]) \
+                 : "v"(sgn))
+    if constexpr (S == 1) EXL3_FMAC8("quad_perm:[1,0,3,2]");
+    else if constexpr (S == 2) EXL3_FMAC8("quad_perm:[2,3,0,1]");
+    else if constexpr (S == 4) EXL3_FMAC8("row_half_mirror");
+    else {
+        static_assert(S == 8, "dpp_block_stage8: S in 1, 2, 4, 8");
+        EXL3_FMAC8("row_ror:8");
+    }
+#undef EXL3_FMAC8
+}
+
 // H128 of one 128-block held by a wave: lane l owns element l in v0 and element
 // l + 64 in v1.  Stages 1..32 pair lanes l and l ^ step, stage 64 pairs v0/v1;
 // each butterfly is (a + b, a - b) with a the lower index, in the reference's

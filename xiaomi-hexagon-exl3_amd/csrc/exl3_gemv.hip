@@ -237,26 +237,44 @@ __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu
                             v[j] = a + b;
                             v[j | st] = a - b;
                         }
-                auto lane_stage = [&](auto sc) {
-                    constexpr int S = decltype(sc)::value;
-                    const float sgn = (pi & S) ? -1.f : 1.f;
-                    float pv[8];
+                // cross-lane stages in signed form: the butterfly sgn v + v' is
+                // sgn (v + sgn v'), so each stage keeps m = m + sgn dpp(m) and the
+                // stage signs multiply into one lane sign, applied with the
+                // 1/sqrt(128) scale; the same roundings as sgn v + v'.  With two or
+                // more units per wave each value is one DPP fmac (dpp_block_stage8:
+                // rows 8 -0.75 us, rows 14 -0.5 us per call at k = 14336); one unit
+                // keeps the compiler's DPP move + fma (the fused blocks were 0.3 us
+                // slower at rows 2)
+                if constexpr (NQ >= 2) {
+                    dpp_block_stage8<1>(v, (pi & 1) ? -1.f : 1.f);
+                    dpp_block_stage8<2>(v, (pi & 2) ? -1.f : 1.f);
+                    dpp_block_stage8<4>(v, (pi & 4) ? -1.f : 1.f);
+                    dpp_block_stage8<8>(v, (pi & 8) ? -1.f : 1.f);
+                } else {
+                    auto lane_stage = [&](auto sc) {
+                        constexpr int S = decltype(sc)::value;
+                        const float sgn = (pi & S) ? -1.f : 1.f;
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) pv[j] = dpp_block_xor<S>(v[j]);
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(v[j], sgn, pv[j]);
-                };
-                lane_stage(std::integral_constant<int, 1>{});
-                lane_stage(std::integral_constant<int, 2>{});
-                lane_stage(std::integral_constant<int, 4>{});
-                lane_stage(std::integral_constant<int, 8>{});
+                        for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(dpp_block_xor<S>(v[j]), sgn, v[j]);
+                    };
+                    lane_stage(std::integral_constant<int, 1>{});
+                    lane_stage(std::integral_constant<int, 2>{});
+                    lane_stage(std::integral_constant<int, 4>{});
+                    lane_stage(std::integral_constant<int, 8>{});
+                }
+                const float scale = (__builtin_popcount(pi & 15) & 1) ? -0.08838834764831844055f
+                                                                       : 0.08838834764831844055f;
                 const int blk = (4 * q + g) * W + wave;
                 if (blk < nblk) {
                     const int kbl = blk / rows, r = blk - kbl * rows;
                     h8 hi, lo;
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
-                        const float e = v[j] * 0.08838834764831844055f;
+                        // opaque product: hi and lo must both come from this binary32
+                        // value (the compiler otherwise rounds x * scale straight to
+                        // fp16 in a v_fma_mix for the lo term and stores hi rounded from
+                        // binary32, which can disagree by one fp16 ulp)
+                        const float e = mul_rn_f32(v[j], scale);
                         hi[j] = (_Float16)e;
                         lo[j] = (_Float16)(e - (float)hi[j]);
                     }
@@ -290,6 +308,7 @@ __global__ __launch_bounds__(kGemvWaves * 64) __attribute__((amdgpu_waves_per_eu
             a *= half_bits_to_float((uint16_t)(ps & 0xffffu));
             b *= half_bits_to_float((uint16_t)(ps >> 16));
             h128_pair(a, b, lane);
+            asm("" : "+v"(a), "+v"(b));  // hi and lo from these binary32 values (as above)
             // elements 2 lane (+1): r4 = lane / 32, kg = lane / 8 % 4, half = lane / 4 % 2,
             // position 2 (lane % 4) (+1) of the 16-byte slot
             const _Float16 ha = (_Float16)a, hb = (_Float16)b;
