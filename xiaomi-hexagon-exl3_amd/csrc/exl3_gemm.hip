@@ -85,29 +85,26 @@ __global__ __launch_bounds__(256) void gemm_xprep_kernel(const uint8_t *__restri
                     v[ps][j] = a + b;
                     v[ps][j | st] = a - b;
                 }
+    // cross-lane stages in signed form, one DPP fmac per value (the GEMV prep's
+    // dpp_block_stage8): the stage signs multiply into one lane sign, applied
+    // with the 1/sqrt(128) scale; the same roundings as sgn v + v'
     auto lane_stage = [&](auto sc) {
         constexpr int S = decltype(sc)::value;
         const float sgn = (i & S) ? -1.f : 1.f;
-        float p[2][8];
-#pragma unroll
-        for (int ps = 0; ps < 2; ++ps)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) p[ps][j] = dpp_block_xor<S>(v[ps][j]);
-#pragma unroll
-        for (int ps = 0; ps < 2; ++ps)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) v[ps][j] = __builtin_fmaf(v[ps][j], sgn, p[ps][j]);
+        dpp_block_stage8<S>(v[0], sgn);
+        dpp_block_stage8<S>(v[1], sgn);
     };
     lane_stage(std::integral_constant<int, 1>{});
     lane_stage(std::integral_constant<int, 2>{});
     lane_stage(std::integral_constant<int, 4>{});
     lane_stage(std::integral_constant<int, 8>{});
+    const float scale = (__builtin_popcount(i & 15) & 1) ? -0.08838834764831844055f : 0.08838834764831844055f;
 #pragma unroll
     for (int ps = 0; ps < 2; ++ps) {
         const int r = 32 * rb + 8 * wave + 4 * ps + g;
         float e[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) e[j] = v[ps][j] * 0.08838834764831844055f;
+        for (int j = 0; j < 8; ++j) e[j] = v[ps][j] * scale;
         uint4 out;
         out.x = (uint32_t)float_to_half_bits(e[0]) | ((uint32_t)float_to_half_bits(e[1]) << 16);
         out.y = (uint32_t)float_to_half_bits(e[2]) | ((uint32_t)float_to_half_bits(e[3]) << 16);
