@@ -478,7 +478,7 @@ exl3_status exl3_hip_decode_batch(const exl3_decode_desc *descs, size_t count, e
         for (size_t i = 0; i < count; ++i) {
             const exl3_decode_desc &d = descs[i];
             if (d.bits != bits) continue;
-            const size_t mwgs = (d.k / 16) * ((d.n / 16 + 15) / 16);
+            const size_t mwgs = ((d.k / 16) * ((d.n / 16 + 15) / 16) + exl3k::kDecodeBlocksPerWg - 1) / exl3k::kDecodeBlocksPerWg;
             if (b.count == exl3k::kDecodeBatchMax || wgs + mwgs > (size_t)0x7fffffff) {
                 const exl3_status st = flush();
                 if (st != EXL3_OK) return st;

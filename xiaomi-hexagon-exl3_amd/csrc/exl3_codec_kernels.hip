@@ -120,18 +120,82 @@ __global__ __launch_bounds__(256) void decode_kernel(const uint8_t *__restrict__
 
 // Several whole matrices of one rate in one launch: workgroup w belongs to the
 // matrix m whose range [wg_begin[m], wg_begin[m + 1]) holds it, and decodes its
-// block (bx, rk) = (local % gx, local / gx) with gx = ceil(n / 256).
+// kDecodeBlocksPerWg consecutive blocks b (bx, rk) = (b % gx, b / gx), gx =
+// ceil(n / 256), from b = kDecodeBlocksPerWg (w - wg_begin[m]): a tile row's
+// neighbouring 256-column blocks.  The next block's stream words are loaded
+// while the current one is decoded, transposed (two LDS buffers) and stored, so
+// a workgroup keeps a block's loads in flight behind its stores.
+template <int K>
+__device__ __forceinline__ bool decode_block_load(const uint8_t *__restrict__ src, int records_layout, size_t k,
+                                                  size_t n, size_t tile_count, size_t gx, size_t b,
+                                                  uint32_t (&w)[RunGeo<K>::NW]) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const size_t bx = b % gx, rk = b / gx, t0 = bx * 16;
+    const int tl = wave * 4 + (lane >> 4);
+    const int c = lane & 7, h = (lane >> 3) & 1;
+    if (t0 + tl >= tile_count) return false;
+    load_run_words<K>(tile_ptr<K>(src, records_layout, k, n, rk, t0 + tl), c, h, w);
+    return true;
+}
+
+template <int K, int CB>
+__device__ __forceinline__ void decode_block_store(const uint32_t (&w)[RunGeo<K>::NW], bool valid, size_t tile_count,
+                                                   size_t gx, size_t b, uint16_t *__restrict__ out, uint16_t *tb) {
+    constexpr int PITCH = kDecodePitch;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const size_t bx = b % gx, rk = b / gx, t0 = bx * 16;
+    const int tl = wave * 4 + (lane >> 4);
+    const int c = lane & 7, h = (lane >> 3) & 1;
+    if (valid) {
+        u4 a1, a2;
+        decode_run<K, CB>(w, a1, a2);
+        const uint32_t p1[4] = {a1.x, a1.y, a1.z, a1.w}, p2[4] = {a2.x, a2.y, a2.z, a2.w};
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int r0 = run_slot_row(h, 2 * v), r1 = run_slot_row(h, 2 * v + 1);
+            tb[r0 * PITCH + tl * 16 + c] = (uint16_t)(p1[v] & 0xffffu);
+            tb[r1 * PITCH + tl * 16 + c] = (uint16_t)(p1[v] >> 16);
+            tb[r0 * PITCH + tl * 16 + c + 8] = (uint16_t)(p2[v] & 0xffffu);
+            tb[r1 * PITCH + tl * 16 + c + 8] = (uint16_t)(p2[v] >> 16);
+        }
+    }
+    __syncthreads();
+    const size_t count = tile_count * 16;  // output row length
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int ch = tid + 256 * i;  // 16 rows x 32 chunks of 8 halves
+        const int row = ch >> 5, col8 = ch & 31;
+        const int tl2 = col8 >> 1;
+        if (t0 + tl2 < tile_count) {
+            const u4 v = *(const u4 *)(tb + row * PITCH + col8 * 8);
+            __builtin_nontemporal_store(v, (u4 *)(out + (rk * 16 + row) * count + (t0 + tl2) * 16 + (col8 & 1) * 8));
+        }
+    }
+}
+
 template <int K, int CB>
 __global__ __launch_bounds__(256) void decode_batch_kernel(DecodeBatch batch, int records_layout) {
-    __shared__ uint16_t tb[16 * kDecodePitch];
+    __shared__ uint16_t tb[2][16 * kDecodePitch];  // one block's transpose while the other's is read
     const unsigned w = blockIdx.x;
     int m = 0;
     for (int i = 1; i < batch.count; ++i)
         if (w >= batch.wg_begin[i]) m = i;
     const size_t k = batch.k[m], n = batch.n[m];
-    const size_t gx = (n / 16 + 15) / 16, local = w - batch.wg_begin[m];
-    decode_block<K, CB>((const uint8_t *)batch.src[m], records_layout, k, n, 0, n / 16, batch.out[m], local % gx,
-                        local / gx, tb);
+    const size_t tiles = n / 16, gx = (tiles + 15) / 16, nblk = (k / 16) * gx;
+    const size_t b0 = (size_t)(w - batch.wg_begin[m]) * kDecodeBlocksPerWg;
+    const uint8_t *src = (const uint8_t *)batch.src[m];
+    uint32_t wa[RunGeo<K>::NW], wb[RunGeo<K>::NW];
+    bool va = decode_block_load<K>(src, records_layout, k, n, tiles, gx, b0, wa), vb = false;
+#pragma unroll
+    for (int j = 0; j < kDecodeBlocksPerWg; j += 2) {  // two register sets: no copy of words in flight
+        if (b0 + j >= nblk) break;  // uniform
+        if (b0 + j + 1 < nblk) vb = decode_block_load<K>(src, records_layout, k, n, tiles, gx, b0 + j + 1, wb);
+        decode_block_store<K, CB>(wa, va, tiles, gx, b0 + j, batch.out[m], tb[0]);
+        if (b0 + j + 1 >= nblk) break;
+        if (j + 2 < kDecodeBlocksPerWg && b0 + j + 2 < nblk)
+            va = decode_block_load<K>(src, records_layout, k, n, tiles, gx, b0 + j + 2, wa);
+        decode_block_store<K, CB>(wb, vb, tiles, gx, b0 + j + 1, batch.out[m], tb[1]);
+    }
 }
 
 template <int K>

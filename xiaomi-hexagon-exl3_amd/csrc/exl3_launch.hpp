@@ -72,11 +72,13 @@ struct GemvTargets {
 
 // Whole matrices of one rate decoded by one launch (decode_batch_kernel).
 constexpr int kDecodeBatchMax = 32;
+// 256-column decode blocks per workgroup of a batch launch (even)
+constexpr unsigned kDecodeBlocksPerWg = 2;
 struct DecodeBatch {
     const void *src[kDecodeBatchMax];
     uint16_t *out[kDecodeBatchMax];
     size_t k[kDecodeBatchMax], n[kDecodeBatchMax];
-    unsigned wg_begin[kDecodeBatchMax];  // first workgroup of each matrix; (k/16) * ceil(n/256) each
+    unsigned wg_begin[kDecodeBatchMax];  // first workgroup of each matrix: ceil((k/16) ceil(n/256) / kDecodeBlocksPerWg) each
     int count;
 };
 
