@@ -437,6 +437,27 @@ def extra_configs(amd, torch, np, synth, stream, args, only_c1=False):
     if only_c1:
         return out
 
+    # the same 4096 x 14336 weight in the other orientation (k=4096 in x n=14336 out, an MLP's
+    # gate/up shape): GEMV at rows 1 and 8, GEMM at M=512 (20 weight copies, 587 MB)
+    k, n, bits = 4096, 14336, 4
+    copies = [records(200 + i, k, n, bits) for i in range(20)]
+    tr = {}
+    for r in (1, 8, 512):
+        x = torch.from_numpy(synth.activations(1200 + r, r, k)).to(dev)
+        y = torch.empty((r, n), dtype=torch.float16, device=dev)
+        ws = amd.new_workspace(k, n, r)
+        it = iter(range(1 << 30))
+        ms = graph_time(torch, stream,
+                        lambda: amd.mul_mat(copies[next(it) % 20], bits, k, n, x, y=y, workspace=ws), 40)
+        gbps = algo_bytes(k, n, bits, r) / (ms * 1e-3) / 1e9
+        tr[f"rows{r}"] = {"call_us": round(ms * 1e3, 2), "gbps": round(gbps, 1),
+                          "frac_hbm": round(gbps / HBM_PEAK_GBPS, 4)}
+        if r == 512:
+            tflops = 2.0 * r * k * n / (ms * 1e-3) / 1e12
+            tr[f"rows{r}"].update({"tflops": round(tflops, 1), "frac_mfma": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)})
+    out["k4096_n14336"] = tr
+    del copies
+
     # C4: projection set of one decoder layer at batch 8, mixed bits, x ~ N(0, sigma 0.5)
     proj = [("q", 2048, 2048, 6), ("k", 2048, 512, 6), ("v", 2048, 512, 6), ("o", 2048, 2048, 6),
             ("gate", 2048, 6144, 4), ("up", 2048, 6144, 4), ("down", 6144, 2048, 3)]
