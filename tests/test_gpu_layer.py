@@ -150,6 +150,26 @@ def test_gemm_unsplit_tiles(amd, oracle, rows):
     assert_layer_close(run(amd, dev(rec), bits, k, n, x), ref, what=f"GEMM k={k} n={n} rows={rows}")
 
 
+def test_k4096_n14336_gemv_and_gemm(amd, oracle):
+    """The 4096 x 14336 weight in the gate/up orientation (k=4096 in, n=14336 out):
+    the GEMV at rows 1 and 8 (112 column groups x 4 k-splits, hi/lo activations,
+    fp32-level accuracy) and the M=512 GEMM (512-row tiles, 2 k-splits) on
+    sampled rows, against the oracle."""
+    k, n, bits = 4096, 14336, 4
+    rec = make_layer(440, k, n, bits)
+    rd = dev(rec)
+    for rows in (1, 8):
+        x = synth.activations(441 + rows, rows, k)
+        ref = oracle.mul_mat(rec, bits, 2, k, n, x, threads=THREADS)
+        _, rl = assert_layer_close(run(amd, rd, bits, k, n, x), ref, what=f"k=4096 n=14336 rows={rows}")
+        assert rl < 1e-5
+    x = synth.activations(450, 512, k)
+    y = run(amd, rd, bits, k, n, x)
+    pick = np.array([0, 1, 255, 256, 511])
+    ref = oracle.mul_mat(rec, bits, 2, k, n, x[pick], threads=THREADS)
+    assert_layer_close(y[pick], ref, what="k=4096 n=14336 M=512 sampled rows")
+
+
 def test_c5_prefill_sampled(amd, oracle):
     """M=512 rows against 4096 x 14336 at 4 bits; 8 sampled rows against the oracle,
     all rows against the GEMV path on the same inputs."""
