@@ -27,9 +27,10 @@ __host__ __device__ inline size_t gemm_xh_offset(int row, int kb, int e, int kbs
     const int ln = (row & 31) + 32 * (kk >> 3);
     return ((((size_t)(row >> 5) * kbs + kb) * 8 + ks) * 64 + ln) * 8 + (kk & 7);
 }
-// Workgroup (kb, rb), 4 waves x 8 rows (two passes of 4); lane 16 g + l holds
-// elements 8 i .. 8 i + 7, i = h128_lane_block(l), of row 32 rb + 8 wave + 4 pass
-// + g.  H128 stages 1, 2 and 4 are inside the lane, 8 .. 64 pair it with the
+// Workgroup (kb, 4 rb + wave) is one wave of 8 rows (two passes of 4; one wave
+// per workgroup spreads a short prep over more CUs than 4-wave workgroups:
+// -0.1 to -0.35 us per call at 24..512 rows); lane 16 g + l holds elements
+// 8 i .. 8 i + 7, i = h128_lane_block(l), of row 32 rb + 8 wave + 4 pass + g.  H128 stages 1, 2 and 4 are inside the lane, 8 .. 64 pair it with the
 // lanes holding i ^ 1 .. 8 (one DPP read each); the lane's eight results are one
 // 16-byte unit of the fragment layout, stored directly.
 template <bool XF16>
@@ -47,12 +48,12 @@ __device__ __forceinline__ void xprep_load(const void *__restrict__ x, const siz
         }
     }
 }
-__global__ __launch_bounds__(256) void gemm_xprep_kernel(const uint8_t *__restrict__ records, int bits,
+__global__ __launch_bounds__(64) void gemm_xprep_kernel(const uint8_t *__restrict__ records, int bits,
                                                          const void *__restrict__ x, int x_f16, size_t x_stride,
                                                          int rows, int kbs, uint16_t *__restrict__ xh16) {
     // i: this lane's 8-element block of the row (h128_lane_block order)
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 4, i = h128_lane_block(lane & 15);
-    const int kb = blockIdx.x, rb = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = blockIdx.y & 3, g = lane >> 4, i = h128_lane_block(lane & 15);
+    const int kb = blockIdx.x, rb = blockIdx.y >> 2;
     const size_t col = (size_t)kb * 128 + 8 * i;
     const uint4 su8 = *(const uint4 *)(records + (size_t)kb * group_bytes(bits) + 2048 * bits + 16 * i);
     const uint32_t suw[4] = {su8.x, su8.y, su8.z, su8.w};
@@ -677,7 +678,7 @@ static hipError_t launch_gemm_k(const void *records, int cb, size_t k, const voi
     const uint8_t *rec = (const uint8_t *)records;
     uint16_t *xh = (uint16_t *)(ws + p.xh_off);
     const int rows_padded = p.mtiles * p.bm;
-    gemm_xprep_kernel<<<dim3(p.kbs, rows_padded / 32), dim3(256), 0, stream>>>(rec, K, x, x_f16, x_stride, (int)rows,
+    gemm_xprep_kernel<<<dim3(p.kbs, rows_padded / 8), dim3(64), 0, stream>>>(rec, K, x, x_f16, x_stride, (int)rows,
                                                                                p.kbs, xh);
     switch (cb) {
     case 0: launch_gemm_kc<K, 0>(rec, k, xh, rows, y, y_f16, y_stride, ws, p, stream, res, res_stride); break;
