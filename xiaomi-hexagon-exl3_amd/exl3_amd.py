@@ -190,9 +190,11 @@ def workspace_bytes(k, n, rows):
     return lib().exl3_hip_mul_mat_workspace_bytes(k, n, rows)
 
 
-def new_workspace(k, n, rows, device="cuda"):
+def new_workspace(k, n, rows, device="cuda", nbytes=None):
+    """A zero-initialised workspace for calls up to (k, n, rows), or of nbytes
+    (for instance group_workspace_bytes of a grouped call) when given."""
     import torch
-    nbytes = max(256, workspace_bytes(k, n, rows))
+    nbytes = max(256, workspace_bytes(k, n, rows) if nbytes is None else nbytes)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
     _check(lib().exl3_hip_workspace_init(_ptr(ws), nbytes, _stream()), "workspace_init")
     return ws
