@@ -539,3 +539,27 @@ def test_fp32_input_range(amd, oracle, rows):
     huge = (x * np.float32(1e6)).astype(np.float32)
     yh = run(amd, rd, bits, k, n, huge)
     assert not np.all(np.isfinite(yh))
+
+
+@pytest.mark.parametrize("bits", range(1, 9))
+def test_every_tile_class_rate_and_codebook(amd, oracle, bits):
+    """Every kernel instance the layer dispatches to, for each rate and codebook:
+    the GEMM's 32-, 64-, 128-, 256- and 512-row tiles (rows 24, 40, 100, 200, 300)
+    and the grouped GEMV's 17..32-row mode with its separate activation prep
+    (two matrices, rows 20), against the oracle at the layer tolerance."""
+    import torch
+    k, n = 512, 256
+    rec = make_layer(1500 + bits, k, n, bits)
+    rec2 = make_layer(1600 + bits, k, n, bits)
+    rd, rd2 = dev(rec), dev(rec2)
+    for cb in range(3):
+        for rows in (24, 40, 100, 200, 300):
+            x = synth.activations(1700 + 10 * bits + cb + rows, rows, k)
+            ref = oracle.mul_mat(rec, bits, cb, k, n, x, threads=THREADS)
+            assert_layer_close(run(amd, rd, bits, k, n, x, cb), ref, what=f"bits={bits} cb={cb} rows={rows}")
+        x = synth.activations(1800 + 10 * bits + cb, 20, k)
+        ys = amd.mul_mat_group([(rd, n), (rd2, n)], bits, k, torch.from_numpy(x).cuda(), codebook=cb)
+        torch.cuda.synchronize()
+        for r, y, tag in ((rec, ys[0], "a"), (rec2, ys[1], "b")):
+            ref = oracle.mul_mat(r, bits, cb, k, n, x, threads=THREADS)
+            assert_layer_close(y.cpu().numpy(), ref, what=f"group {tag} bits={bits} cb={cb} rows=20")
