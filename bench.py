@@ -385,24 +385,32 @@ def xs8_slice(xs, r):
     return xs[8][:r]
 
 
-def graph_time(torch, stream, fn, per_graph, replays=3):
-    """Mean ms of one fn() call: a HIP graph holding per_graph calls (fn may
-    rotate through weight copies) replayed `replays` times between HIP events."""
+def graph_time(torch, stream, fn, per_graph, replays=5, warm_ms=10.0):
+    """ms of one fn() call: a HIP graph holding per_graph calls (fn may rotate
+    through weight copies), replayed untimed for warm_ms (steady clocks after the
+    previous configuration), then `replays` times between HIP events; the median
+    replay over per_graph."""
     fn()
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         for _ in range(per_graph):
             fn()
+    t0 = time.perf_counter()
     g.replay()
     torch.cuda.synchronize()
-    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s_ev.record(stream)
-    for _ in range(replays):
+    while time.perf_counter() - t0 < warm_ms * 1e-3:
         g.replay()
-    e_ev.record(stream)
-    torch.cuda.synchronize()
-    return s_ev.elapsed_time(e_ev) / (replays * per_graph)
+        torch.cuda.synchronize()
+    times = []
+    for _ in range(replays):
+        s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s_ev.record(stream)
+        g.replay()
+        e_ev.record(stream)
+        torch.cuda.synchronize()
+        times.append(s_ev.elapsed_time(e_ev) / per_graph)
+    return sorted(times)[len(times) // 2]
 
 
 def extra_configs(amd, torch, np, synth, stream, args, only_c1=False):
@@ -458,6 +466,21 @@ def extra_configs(amd, torch, np, synth, stream, args, only_c1=False):
     out["k4096_n14336"] = tr
     del copies
 
+    # the vocabulary head as a GEMV: k=2048 in x n=151,936 out, 6 bits, batch 1 (a decode
+    # step's output layer; 2 weight copies, 480 MB: past the 256 MB MALL)
+    k, n, bits = 2048, 151936, 6
+    copies = [records(300 + i, k, n, bits) for i in range(2)]
+    x = torch.from_numpy(synth.activations(1300, 1, k)).to(dev)
+    y = torch.empty((1, n), dtype=torch.float16, device=dev)
+    ws = amd.new_workspace(k, n, 1)
+    it = iter(range(1 << 30))
+    ms = graph_time(torch, stream, lambda: amd.mul_mat(copies[next(it) % 2], bits, k, n, x, y=y, workspace=ws), 20)
+    gbps = algo_bytes(k, n, bits, 1) / (ms * 1e-3) / 1e9
+    out["head_k2048_n151936_b1"] = {"call_us": round(ms * 1e3, 2), "gbps": round(gbps, 1),
+                                    "frac_hbm": round(gbps / HBM_PEAK_GBPS, 4), "bits": bits,
+                                    "note": "graph replay, 2 weight copies"}
+    del copies
+
     # C4: projection set of one decoder layer at batch 8, mixed bits, x ~ N(0, sigma 0.5)
     proj = [("q", 2048, 2048, 6), ("k", 2048, 512, 6), ("v", 2048, 512, 6), ("o", 2048, 2048, 6),
             ("gate", 2048, 6144, 4), ("up", 2048, 6144, 4), ("down", 6144, 2048, 3)]
@@ -508,13 +531,13 @@ def extra_configs(amd, torch, np, synth, stream, args, only_c1=False):
     def sweep_each():
         for (k2, n2), b2, p2, o2 in zip(mats, bits_c2, packed, outs):
             amd.decode(p2, int(b2), k2, n2, codebook=CB, out=o2)
-    ms_each = graph_time(torch, stream, sweep_each, 1, replays=3)
+    ms_each = graph_time(torch, stream, sweep_each, 1)
     # one exl3_hip_decode_batch call: the matrices of each rate share launches
     batch = [(p2, int(b2), k2, n2, o2) for (k2, n2), b2, p2, o2 in zip(mats, bits_c2, packed, outs)]
 
     def sweep():
         amd.decode_batch(batch, codebook=CB)
-    ms = graph_time(torch, stream, sweep, 1, replays=3)
+    ms = graph_time(torch, stream, sweep, 1)
     c2_bytes = sum(k2 * n2 * int(b2) // 8 + 2 * k2 * n2 for (k2, n2), b2 in zip(mats, bits_c2))
     wsum = sum(k2 * n2 for k2, n2 in mats)
     out["c2_dequant_sweep"] = {"gbps": round(c2_bytes / (ms * 1e-3) / 1e9, 1), "sweep_ms": round(ms, 3),
