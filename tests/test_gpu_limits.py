@@ -76,3 +76,20 @@ def test_rows_beyond_the_reference_chunk_and_at_the_limit(amd, oracle):
     with pytest.raises(amd.Exl3Error) as e:
         amd.mul_mat(rec, 4, 128, 128, x, codebook=MUL1)
     assert e.value.status == amd.INVAL_PARAMS
+
+
+def test_decode_at_the_limits(amd, oracle):
+    """exl3_hip_decode and exl3_hip_decode_batch of the largest k and the largest
+    n, bit for bit against the oracle's decode_inner (src/exl3_codec.cpp:117-145)."""
+    import torch
+    for k, n, bits in [(65536, 256, 5), (128, 1048576, 3)]:
+        print(f"  decode k={k} n={n} bits={bits}", flush=True)
+        p = synth.packed_tiles(2400 + bits, k, n, bits)
+        pd = dev(p)
+        want = oracle.decode_inner(p, k, n, bits, MUL1)
+        got = amd.decode(pd, bits, k, n, codebook=MUL1)
+        torch.cuda.synchronize()
+        assert np.array_equal(got.cpu().numpy().view(np.uint16), want)
+        (batch,) = amd.decode_batch([(pd, bits, k, n, None)], codebook=MUL1)
+        torch.cuda.synchronize()
+        assert torch.equal(batch, got)
