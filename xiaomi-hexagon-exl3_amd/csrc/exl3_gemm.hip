@@ -546,12 +546,14 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const uint16_t *__rest
                     a1 += ((const float *)res)[ro + lane + 64];
                 }
             }
+            // non-temporal: k = 4096, n = 14336 M=512 -0.6 us, k = 2048, n = 6144 rows 256
+            // -0.3 us, the rest within +-0.1 us
             if (y_f16) {
-                ((uint16_t *)y)[o + lane] = float_to_half_bits(a0);
-                ((uint16_t *)y)[o + lane + 64] = float_to_half_bits(a1);
+                __builtin_nontemporal_store(float_to_half_bits(a0), (uint16_t *)y + o + lane);
+                __builtin_nontemporal_store(float_to_half_bits(a1), (uint16_t *)y + o + lane + 64);
             } else {
-                ((float *)y)[o + lane] = a0;
-                ((float *)y)[o + lane + 64] = a1;
+                __builtin_nontemporal_store(a0, (float *)y + o + lane);
+                __builtin_nontemporal_store(a1, (float *)y + o + lane + 64);
             }
         }
     }
